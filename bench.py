@@ -1,0 +1,231 @@
+"""Benchmark of the HIP kernel path on one MI355X: prints ONE JSON line.
+
+Headline (`value`): the fused q/k RMSNorm + RoPE + paged-KV write at T = 8192 tokens, Qwen3-0.6B attention shape
+(16 q heads, 8 kv heads, head_dim 128), in GB/s of algorithmic bytes:
+  qkv a strided view of a [T, 4096 + 64] bf16 buffer; positions contiguous over 4 sequences of T/4 tokens; a
+  512-block x 256-slot paged cache; every slot valid (the reference's microbenchmark layout); write_k False.
+  bytes/launch = T * (4096 q read + 4096 q_out write + 8 position + 4 slot + 512 cos/sin)
+                 + n_valid * (2048 k read + 2048 v read + 2048 k cache write + 2048 v cache write) + 512 weights
+               = 16 908 * T + 512 with every slot valid (the reference's formula, scripts/bench_qk_rope_kv.py:50-52).
+One step = one launch over the T tokens. NSETS input/output sets (each with its own block table) rotate from
+launch to launch so that the working set (> 256 MB) does not stay in the Infinity Cache; the K timed launches are
+replayed from HIP graphs and timed with HIP events on the stream they run on.
+
+Also reported (under "extra"): the same kernel at T = 1, 32, 2048; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
+(hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048, in TFLOP/s.
+The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
+sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 8192] [--no-cpu] [--no-extra]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nano-vllm-triton-kernels_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "qk-norm+RoPE+KV-write GB/s (%HBM peak) at T=8192; bf16 GEMM TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+HQ, HKV, D, MAX_POS, THETA, BLOCK, EPS = 16, 8, 128, 40960, 1e6, 256, 1e-6
+NUM_BLOCKS = 512
+PAD = 64
+NSETS = 4
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qk_norm_rope_kv_t8192_traffic.json")
+
+
+def fused_bytes(T, n_valid, write_k=False):
+    return T * (HQ * D * 2 * 2 + 8 + 4 + D * 4) + n_valid * (4 * HKV * D * 2) + (HKV * D * 2 if write_k else 0) * T \
+        + 2 * D * 2
+
+
+def block_table_slots(T, g, torch):
+    """Slots of 4 sequences of T/4 tokens in random distinct blocks, and their contiguous positions."""
+    nseq = min(4, T)
+    lens = [T // nseq + (1 if i < T % nseq else 0) for i in range(nseq)]
+    perm = torch.randperm(NUM_BLOCKS, generator=g)
+    slots, positions, used = [], [], 0
+    for n in lens:
+        nb = (n + BLOCK - 1) // BLOCK
+        blocks = perm[used:used + nb]
+        used += nb
+        off = torch.arange(n)
+        slots.append(blocks[off // BLOCK] * BLOCK + off % BLOCK)
+        start = int(torch.randint(0, 4096, (1,), generator=g))
+        positions.append(start + off)
+    return torch.cat(slots).to(torch.int32), torch.cat(positions).to(torch.int64)
+
+
+class FusedWorkload:
+    def __init__(self, T, dev, torch, oracle, seed=0):
+        g = torch.Generator("cpu").manual_seed(seed)
+        self.T = T
+        self.sets = []
+        for _ in range(NSETS):
+            buf = torch.randn(T, (HQ + 2 * HKV) * D + PAD, generator=g).to(torch.bfloat16).to(dev)
+            q = buf[:, :HQ * D].view(T, HQ, D)
+            k = buf[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D)
+            v = buf[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].view(T, HKV, D)
+            slots, positions = block_table_slots(T, g, torch)
+            self.sets.append(dict(buf=buf, q=q, k=k, v=v, slots=slots.to(dev), positions=positions.to(dev)))
+        self.q_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev)
+        self.k_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev)
+        self.cos_sin = oracle.rope_cos_sin_cache(D, MAX_POS, THETA).to(dev)
+        self.k_cache = torch.zeros(NUM_BLOCKS, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.n_valid = T
+
+    def call(self, i, qk_norm_rope_kv):
+        s = self.sets[i % NSETS]
+        return qk_norm_rope_kv(s["q"], s["k"], s["v"], s["positions"], self.q_w, self.k_w, EPS, self.cos_sin,
+                               self.k_cache, self.v_cache, s["slots"], False)
+
+
+def time_graph(torch, fn, n_calls, steps, warmup):
+    """Records n_calls calls of fn(i) into one HIP graph, replays it (warmup + steps calls, rounded up to whole
+    replays) and returns the average milliseconds per call, timed with events on the replay stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n_calls):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n_calls):
+            fn(i)
+    reps_warm = max(1, -(-warmup // n_calls))
+    reps = max(1, -(-steps // n_calls))
+    for _ in range(reps_warm):
+        graph.replay()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / (reps * n_calls), reps * n_calls
+
+
+def cpu_baseline(torch, oracle, T, budget_s=12.0):
+    """The oracle (torch CPU, fp32 math) on the same fused workload, timed on the host cores."""
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    g = torch.Generator("cpu").manual_seed(1)
+    buf = torch.randn(T, (HQ + 2 * HKV) * D + PAD, generator=g).to(torch.bfloat16)
+    q = buf[:, :HQ * D].view(T, HQ, D)
+    k = buf[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D)
+    v = buf[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].view(T, HKV, D)
+    slots, positions = block_table_slots(T, g, torch)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cos_sin = oracle.rope_cos_sin_cache(D, MAX_POS, THETA)
+    kc = torch.zeros(NUM_BLOCKS, BLOCK, HKV, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    run = lambda: oracle.qk_norm_rope_kv(q, k, v, positions, qw, kw, EPS, cos_sin, kc, vc, slots, False)
+    run()  # warm up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(fused_bytes(T, T) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle qk_norm_rope_kv (torch CPU fp32) at T={T}, {len(times)} calls in ~{budget_s:.0f} s, "
+                      f"median {med * 1e3:.1f} ms/call, {torch.get_num_threads()} threads"}
+
+
+def extras(torch, oracle, kernels, dev, steps):
+    out = {}
+    for T in (1, 32, 2048):
+        wl = FusedWorkload(T, dev, torch, oracle, seed=T)
+        ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, max(40, steps), 20)
+        out[f"qk_norm_rope_kv_T{T}"] = {"us": round(ms * 1e3, 3),
+                                        "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1)}
+    T, H, I = 8192, 1024, 3072
+    g = torch.Generator("cpu").manual_seed(2)
+    xs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+    rs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+    gus = [torch.randn(T, 2 * I, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+    for name, fn, nbytes in (
+            ("rms_norm_T8192", lambda i: kernels.rms_norm(xs[i], w, EPS), (2 * T * H + H) * 2),
+            ("fused_add_rms_norm_T8192", lambda i: kernels.fused_add_rms_norm(xs[i], rs[i], w, EPS),
+             (4 * T * H + H) * 2),
+            ("silu_and_mul_T8192", lambda i: kernels.silu_and_mul(gus[i]), 3 * T * I * 2)):
+        ms, _ = time_graph(torch, fn, NSETS, max(40, steps), 20)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    del xs, rs, gus
+    for layer, (K, N) in {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024),
+                          "o_proj": (2048, 1024)}.items():
+        M = 2048
+        a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+        wt = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
+        b = wt.t()
+        ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 4, max(40, steps), 20)
+        tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+        ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, wt), 4, max(40, steps), 20)
+        out[f"gemm_bf16_{layer}_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                           "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
+                                           "torch_linear_us": round(ms_ref * 1e3, 2)}
+    return out
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--tokens", type=int, default=8192)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="only the headline kernel")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the kernel path has no collective; "
+              "see the sharding notes in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import oracle
+    import nanovllm_hip.kernels as kernels
+
+    dev = torch.device("cuda:0")
+    T = args.tokens
+    wl = FusedWorkload(T, dev, torch, oracle)
+    ms, steps_done = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, args.steps, args.warmup)
+    nbytes = fused_bytes(T, wl.n_valid)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    result = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps_done,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"qk_norm_rope_kv Qwen3-0.6B attention (Hq 16, Hkv 8, D 128), T={T}, qkv view of "
+                               f"[T, 4096+{PAD}], 4 sequences, 512x256-slot paged KV, all slots valid, write_k=False",
+                   "tokens": T, "bytes_per_step": nbytes, "rotating_sets": NSETS},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+    }
+    if not args.no_extra:
+        result["extra"] = extras(torch, oracle, kernels, dev, args.steps)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(torch, oracle, T)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

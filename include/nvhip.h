@@ -1,0 +1,96 @@
+/*
+ * nvhip.h — C ABI of the MI355X (gfx950) kernels behind nano-vllm's kernel_backend="hip".
+ *
+ * One entry point per kernel family of nano-vllm's nanovllm/kernels/ package. Every entry point
+ *   - takes raw device pointers, int64 sizes/strides (in elements), scalars and a hipStream_t (passed as void*);
+ *   - launches asynchronously on that stream and returns 0 on success, or a negative NVHIP_E* code;
+ *   - never allocates, synchronises or touches global mutable device state, so it may be recorded into a HIP graph;
+ *   - on failure stores a message readable with nvhip_last_error() (thread-local, valid until the next call).
+ * bf16 tensors are passed as void* holding IEEE bfloat16 values (torch.bfloat16).
+ * Size 0 (T == 0, rows == 0, M*N == 0) is a valid no-op that launches nothing.
+ */
+#ifndef NVHIP_H
+#define NVHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NVHIP_OK 0
+#define NVHIP_EINVAL -1   /* bad argument: null pointer, bad size/stride/shape, unsupported dtype */
+#define NVHIP_ELAUNCH -2  /* the HIP runtime refused the launch */
+
+#define NVHIP_DTYPE_F32 0
+#define NVHIP_DTYPE_BF16 1
+
+#define NVHIP_PREC_IEEE 0 /* fp32 inputs used as they are */
+#define NVHIP_PREC_TF32 1 /* fp32 inputs rounded to a 10-bit mantissa (tf32) before the products */
+
+/* ABI version (bumped on any signature change). */
+int nvhip_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* nvhip_last_error(void);
+
+/*
+ * Fused per-head q/k RMSNorm + RoPE + paged KV-cache write (Qwen3 attention pre-segment).
+ * Replaces qk_norm_rope_kv() of nanovllm/kernels/qk_norm_rope_kv.py:92-125 (its Triton kernel :45-82).
+ *   q [T, Hq, D], k, v [T, Hkv, D] bf16: row t at ptr + t*{q,k,v}_stride, head h at + h*D, elements contiguous.
+ *   positions [T] int64 (clamped to [0, max_pos)); cos_sin [max_pos, D] fp32 rows of (cos | sin), row stride
+ *   cos_sin_stride; q_weight, k_weight [D] bf16; eps the RMSNorm epsilon.
+ *   q_out [T, Hq, D] bf16 contiguous (always written).
+ *   k_out [T, Hkv, D] bf16 contiguous, or NULL (= write_k False).
+ *   k_cache, v_cache [num_slots, Hkv, D] bf16 contiguous (blocks x block_size slots), or both NULL (no store; then
+ *   slot_mapping may be NULL). slot_mapping [T] int32: token t goes to slot slot_mapping[t]; slots outside
+ *   [0, num_slots) (the padding value -1) are skipped.
+ * Supported D: 64, 128, 256. Numerics: see the kernel source.
+ */
+int nvhip_qk_norm_rope_kv_bf16(void* q_out, void* k_out, const void* q, const void* k, const void* v,
+                               int64_t q_stride, int64_t k_stride, int64_t v_stride, const int64_t* positions,
+                               const int32_t* slot_mapping, const void* q_weight, const void* k_weight,
+                               const float* cos_sin, int64_t cos_sin_stride, int64_t max_pos, void* k_cache,
+                               void* v_cache, int64_t num_slots, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                               float eps, void* stream);
+
+/*
+ * RMSNorm over the last dim: y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
+ * Replaces rms_norm() of nanovllm/kernels/rms_norm.py:83-98 (its Triton kernel :34-54).
+ *   x: groups x rows_per_group rows of n bf16; row (g, r) at x + g*group_stride + r*row_stride (elements
+ *   contiguous). A 2-D [rows, n] input is groups=rows, rows_per_group=1, row_stride=0.
+ *   y: [groups*rows_per_group, n] bf16 contiguous. w: [n] bf16.
+ */
+int nvhip_rms_norm_bf16(void* y, const void* x, const void* w, int64_t groups, int64_t rows_per_group,
+                        int64_t group_stride, int64_t row_stride, int64_t n, float eps, void* stream);
+
+/*
+ * Add + RMSNorm: s = fp32(x) + fp32(residual); residual_out = bf16(s); y = bf16(bf16(s * rsqrt(mean(s^2)+eps)) * w).
+ * Replaces fused_add_rms_norm() of nanovllm/kernels/rms_norm.py:101-111 (its Triton kernel :57-80).
+ *   x, residual [rows, n] bf16 with row strides x_stride, r_stride (elements contiguous).
+ *   y, residual_out [rows, n] bf16 contiguous. residual_out may equal residual (in place) when r_stride == n.
+ */
+int nvhip_add_rms_norm_bf16(void* y, void* residual_out, const void* x, const void* residual, const void* w,
+                            int64_t rows, int64_t x_stride, int64_t r_stride, int64_t n, float eps, void* stream);
+
+/*
+ * SiLU x Mul: out = bf16(bf16(silu(fp32(gate))) * up), gate = x[:, :n], up = x[:, n:2n].
+ * Replaces silu_and_mul() of nanovllm/kernels/swiglu.py:34-43 (its Triton kernel :19-31).
+ *   x [rows, 2n] bf16, row stride x_stride (elements contiguous); out [rows, n] bf16 contiguous.
+ */
+int nvhip_silu_mul_bf16(void* out, const void* x, int64_t rows, int64_t x_stride, int64_t n, void* stream);
+
+/*
+ * GEMM: C[M, N] = A[M, K] @ B[K, N], fp32 accumulation, C in the input dtype (fp32 or bf16).
+ * Replaces matmul() of nanovllm/kernels/matmul.py:84-99 (its Triton kernel :33-81).
+ *   Element (i, j) of X lives at X + i*s_x0 + j*s_x1 (any non-negative strides, e.g. B = W.t() of a [N, K]
+ *   weight: sbk = 1, sbn = K). precision: NVHIP_PREC_IEEE or NVHIP_PREC_TF32 (fp32 only; ignored for bf16).
+ */
+int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
+                 int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype, int precision, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVHIP_H */

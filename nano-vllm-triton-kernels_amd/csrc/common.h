@@ -1,0 +1,105 @@
+// Shared device helpers and host-side argument checking for the nvhip kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "nvhip.h"
+
+namespace nvhip {
+
+// ---------------------------------------------------------------- host: errors
+
+void set_error(const std::string& msg);
+void clear_error();
+
+// Records msg and returns NVHIP_EINVAL.
+int invalid(const std::string& msg);
+
+// Checks the launch that was just issued; NVHIP_OK or NVHIP_ELAUNCH with the runtime's message.
+int check_launch(const char* kernel);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------- device: bf16 <-> fp32
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 bits -> fp32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+// Two fp32 -> two bf16 packed in one word (a in the low half), round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 v = __builtin_convertvector((f32x2){a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float a) { return uint16_t(pack_bf16x2(a, 0.0f)); }
+
+// fp32 value rounded to the nearest bf16 (as an fp32): the .to(torch.bfloat16) of the torch code.
+__device__ __forceinline__ float round_bf16(float a) { return bf16_lo(pack_bf16x2(a, 0.0f)); }
+
+// 8 bf16 (16 bytes) <-> 8 fp32.
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(v[i]);
+    f[2 * i + 1] = bf16_hi(v[i]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
+// Loads/stores of 8 consecutive bf16. ALIGNED: one 16-byte access (pointer must be 16-byte aligned);
+// otherwise 8 two-byte accesses.
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load8(const uint16_t* p) {
+  if constexpr (ALIGNED) {
+    return *reinterpret_cast<const u32x4*>(p);
+  } else {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = uint32_t(p[2 * i]) | (uint32_t(p[2 * i + 1]) << 16);
+    return v;
+  }
+}
+template <bool ALIGNED>
+__device__ __forceinline__ void store8(uint16_t* p, const u32x4& v) {
+  if constexpr (ALIGNED) {
+    *reinterpret_cast<u32x4*>(p) = v;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[2 * i] = uint16_t(v[i]);
+      p[2 * i + 1] = uint16_t(v[i] >> 16);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- device: reductions
+
+// Sum over aligned groups of LANES consecutive lanes of a wave64 (LANES a power of two, 1..64). Every lane of a
+// group gets the same (bitwise) result. Groups of up to 16 use DPP (quad_perm, row_half_mirror, row_mirror),
+// wider groups finish with ds_swizzle / bpermute shuffles.
+template <int LANES>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(LANES >= 1 && LANES <= 64 && (LANES & (LANES - 1)) == 0, "LANES must be a power of two <= 64");
+  if constexpr (LANES >= 2) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  if constexpr (LANES >= 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  if constexpr (LANES >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  if constexpr (LANES >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  if constexpr (LANES >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (LANES >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+}  // namespace nvhip

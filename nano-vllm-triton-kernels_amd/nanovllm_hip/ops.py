@@ -1,0 +1,158 @@
+"""PyTorch custom ops (namespace `nvhip`) over the C-ABI kernels of libnvhip.so.
+
+Each op has a CUDA (= ROCm/HIP device) implementation that allocates its outputs with torch's caching allocator and
+launches the kernel on torch's current stream through ctypes, and a fake (meta) implementation so torch.compile and
+graph capture can trace it. There is no CPU implementation: CPU tensors raise in the dispatcher.
+
+The user-facing functions with the reference's signatures are in nanovllm_hip.kernels; these ops take the already
+validated, normalised arguments.
+"""
+import torch
+
+from nanovllm_hip import _lib
+
+_DEF = torch.library.Library("nvhip", "DEF")
+
+_DEF.define(
+    "qk_norm_rope_kv(Tensor q, Tensor k, Tensor v, Tensor positions, Tensor q_weight, Tensor k_weight, float eps, "
+    "Tensor cos_sin_cache, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? slot_mapping, bool write_k) "
+    "-> (Tensor, Tensor)")
+_DEF.define("rms_norm(Tensor x, Tensor w, float eps) -> Tensor")
+_DEF.define("fused_add_rms_norm(Tensor x, Tensor residual, Tensor w, float eps) -> (Tensor, Tensor)")
+_DEF.define("fused_add_rms_norm_(Tensor x, Tensor(a!) residual, Tensor w, float eps) -> Tensor")
+_DEF.define("silu_and_mul(Tensor x) -> Tensor")
+_DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
+
+
+# ------------------------------------------------------------------ qk_norm_rope_kv
+
+def _qk_outputs(q, k, write_k):
+    T, Hq, D = q.shape
+    q_out = q.new_empty((T, Hq, D))
+    k_out = k.new_empty((T, k.shape[1], D)) if write_k else k.new_empty((0,))
+    return q_out, k_out
+
+
+def _qk_norm_rope_kv_impl(q, k, v, positions, q_weight, k_weight, eps, cos_sin_cache, k_cache, v_cache,
+                          slot_mapping, write_k):
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    q_out, k_out = _qk_outputs(q, k, write_k)
+    store = k_cache.numel() > 0
+    cs = cos_sin_cache
+    status = _lib.lib().nvhip_qk_norm_rope_kv_bf16(
+        q_out.data_ptr(), k_out.data_ptr() if write_k else None,
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
+        positions.data_ptr(), slot_mapping.data_ptr() if store else None,
+        q_weight.data_ptr(), k_weight.data_ptr(), cs.data_ptr(), cs.stride(0), cs.shape[0],
+        k_cache.data_ptr() if store else None, v_cache.data_ptr() if store else None,
+        k_cache.numel() // (Hkv * D) if store else 0,
+        T, Hq, Hkv, D, float(eps), _lib.stream_of(q))
+    _lib.check(status, "qk_norm_rope_kv")
+    return q_out, k_out
+
+
+_DEF.impl("qk_norm_rope_kv", _qk_norm_rope_kv_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::qk_norm_rope_kv")
+def _qk_norm_rope_kv_fake(q, k, v, positions, q_weight, k_weight, eps, cos_sin_cache, k_cache, v_cache,
+                          slot_mapping, write_k):
+    return _qk_outputs(q, k, write_k)
+
+
+# ------------------------------------------------------------------ rms_norm / fused_add_rms_norm
+
+def _rms_norm_impl(x, w, eps):
+    n = x.shape[-1]
+    if x.dim() == 2:
+        groups, rows_per_group, group_stride, row_stride = x.shape[0], 1, x.stride(0), 0
+    else:
+        groups, rows_per_group, group_stride, row_stride = x.shape[0], x.shape[1], x.stride(0), x.stride(1)
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    status = _lib.lib().nvhip_rms_norm_bf16(y.data_ptr(), x.data_ptr(), w.data_ptr(), groups, rows_per_group,
+                                            group_stride, row_stride, n, float(eps), _lib.stream_of(x))
+    _lib.check(status, "rms_norm")
+    return y
+
+
+_DEF.impl("rms_norm", _rms_norm_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::rms_norm")
+def _rms_norm_fake(x, w, eps):
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+def _add_rms(x, residual, w, eps, res_out):
+    rows, n = x.shape
+    y = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    status = _lib.lib().nvhip_add_rms_norm_bf16(y.data_ptr(), res_out.data_ptr(), x.data_ptr(), residual.data_ptr(),
+                                                w.data_ptr(), rows, x.stride(0), residual.stride(0), n, float(eps),
+                                                _lib.stream_of(x))
+    _lib.check(status, "fused_add_rms_norm")
+    return y
+
+
+def _fused_add_rms_norm_impl(x, residual, w, eps):
+    s = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    return _add_rms(x, residual, w, eps, s), s
+
+
+def _fused_add_rms_norm_inplace_impl(x, residual, w, eps):
+    return _add_rms(x, residual, w, eps, residual)
+
+
+_DEF.impl("fused_add_rms_norm", _fused_add_rms_norm_impl, "CUDA")
+_DEF.impl("fused_add_rms_norm_", _fused_add_rms_norm_inplace_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::fused_add_rms_norm")
+def _fused_add_rms_norm_fake(x, residual, w, eps):
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device), torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+@torch.library.register_fake("nvhip::fused_add_rms_norm_")
+def _fused_add_rms_norm_inplace_fake(x, residual, w, eps):
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+# ------------------------------------------------------------------ silu_and_mul
+
+def _silu_and_mul_impl(x):
+    rows, n = x.shape[0], x.shape[1] // 2
+    out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    status = _lib.lib().nvhip_silu_mul_bf16(out.data_ptr(), x.data_ptr(), rows, x.stride(0), n, _lib.stream_of(x))
+    _lib.check(status, "silu_and_mul")
+    return out
+
+
+_DEF.impl("silu_and_mul", _silu_and_mul_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::silu_and_mul")
+def _silu_and_mul_fake(x):
+    return torch.empty((x.shape[0], x.shape[1] // 2), dtype=x.dtype, device=x.device)
+
+
+# ------------------------------------------------------------------ matmul
+
+def _matmul_impl(a, b, input_precision):
+    M, K = a.shape
+    N = b.shape[1]
+    c = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    dtype = _lib.DTYPE_BF16 if a.dtype == torch.bfloat16 else _lib.DTYPE_F32
+    prec = _lib.PREC_TF32 if input_precision == "tf32" else _lib.PREC_IEEE
+    status = _lib.lib().nvhip_matmul(c.data_ptr(), a.data_ptr(), b.data_ptr(), M, N, K, a.stride(0), a.stride(1),
+                                     b.stride(0), b.stride(1), c.stride(0), c.stride(1), dtype, prec,
+                                     _lib.stream_of(a))
+    _lib.check(status, "matmul")
+    return c
+
+
+_DEF.impl("matmul", _matmul_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::matmul")
+def _matmul_fake(a, b, input_precision):
+    return torch.empty((a.shape[0], b.shape[1]), dtype=a.dtype, device=a.device)

@@ -1,0 +1,33 @@
+"""CPU oracle for the nano-vllm kernel path — TEST INFRASTRUCTURE ONLY.
+
+A plain-torch fp32 restatement of the reference's eager torch code (the code its Triton kernels replace), run on
+CPU tensors with the same rounding points. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import it, and only as the checker or the timed CPU baseline; the product path (nanovllm_hip) never calls it.
+
+Functions and the reference code each one follows (paths in R3pere/nano-vllm-triton-kernels):
+  rms_forward        nanovllm/layers/layernorm.py:20-30   (RMSNorm.rms_forward)
+  add_rms_forward    nanovllm/layers/layernorm.py:32-44   (RMSNorm.add_rms_forward)
+  rope_cos_sin_cache nanovllm/layers/rotary_embedding.py:19-35 (RotaryEmbedding.__init__ cache)
+  apply_rotary_emb   nanovllm/layers/rotary_embedding.py:6-14
+  rotary_forward     nanovllm/layers/rotary_embedding.py:37-48 (RotaryEmbedding.forward)
+  store_kvcache      nanovllm/layers/attention.py:11-41   (store_kvcache_kernel / store_kvcache)
+  qk_norm_rope_kv    nanovllm/models/qwen3.py:89-105 + nanovllm/layers/attention.py:64-76 (the unfused composition
+                     that nanovllm/kernels/qk_norm_rope_kv.py:92-125 replaces)
+  silu_and_mul       nanovllm/layers/activation.py:15-18
+  matmul_fp64        tests/test_kernels_matmul.py:52 (A.double() @ B.double())
+
+How each is pinned (tests/test_oracle.py): closed forms in float64, hand-computed known answers, invariants
+(identity rotation, norm preservation, relative-position dependence, scale invariance), and brute-force loops on
+tiny inputs. The reference ships no golden vectors for this path.
+"""
+from oracle.torch_ref import (  # noqa: F401
+    add_rms_forward,
+    apply_rotary_emb,
+    matmul_fp64,
+    qk_norm_rope_kv,
+    rms_forward,
+    rope_cos_sin_cache,
+    rotary_forward,
+    silu_and_mul,
+    store_kvcache,
+)

@@ -1,0 +1,94 @@
+"""Torch restatement of the reference's eager code for the kernel path (TEST INFRASTRUCTURE ONLY: see __init__).
+
+Every function takes and returns torch tensors and runs on whatever device its inputs are on (CPU for the oracle;
+the GPU tests may also run it on the GPU to get torch's own GPU rounding). bf16 activations, fp32 arithmetic, and
+a bf16 rounding exactly where the reference's torch code has a `.to(bfloat16)` or a bf16 multiply.
+"""
+import torch
+
+BF16 = torch.bfloat16
+
+
+def rms_forward(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm of the last dim (layers/layernorm.py:20-30): y = bf16(x * rsqrt(mean(x^2) + eps)) * weight.
+
+    x: bf16 [..., n] (any strides); weight: bf16 [n]. The fp32 normalised value is rounded to x's dtype before
+    the weight multiply, and that multiply is a bf16 x bf16 product (computed in fp32, rounded to bf16)."""
+    xf = x.to(torch.float32)
+    mean_sq = xf.pow(2).mean(dim=-1, keepdim=True)
+    normed = xf * torch.rsqrt(mean_sq + eps)
+    return normed.to(x.dtype).mul_(weight)  # in place: the product keeps x's dtype whatever weight's dtype
+
+
+def add_rms_forward(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """Add + RMSNorm (layers/layernorm.py:32-44). Returns (y, new_residual).
+
+    s = fp32(x) + fp32(residual); new_residual = bf16(s); y = RMSNorm of the *unrounded* fp32 s."""
+    s = x.to(torch.float32) + residual.to(torch.float32)
+    new_residual = s.to(x.dtype)
+    mean_sq = s.pow(2).mean(dim=-1, keepdim=True)
+    normed = s * torch.rsqrt(mean_sq + eps)
+    return normed.to(x.dtype).mul_(weight), new_residual
+
+
+def rope_cos_sin_cache(head_size: int, max_position: int, base: float) -> torch.Tensor:
+    """The rotary table (layers/rotary_embedding.py:19-35): [max_position, 1, head_size] fp32, row p = (cos | sin)
+    of p * inv_freq, inv_freq[i] = 1 / base^(2i / head_size), all computed in fp32."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_size, 2, dtype=torch.float32) / head_size))
+    pos = torch.arange(max_position, dtype=torch.float32)
+    angles = pos[:, None] * inv_freq[None, :]  # fp32 outer product, as the reference's einsum "i,j -> ij"
+    return torch.cat((angles.cos(), angles.sin()), dim=-1).unsqueeze(1)
+
+
+def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE (layers/rotary_embedding.py:6-14): halves x1, x2 of fp32(x);
+    y1 = x1*cos - x2*sin, y2 = x2*cos + x1*sin, each product a separately rounded fp32 tensor; result in x's dtype."""
+    x1, x2 = torch.chunk(x.to(torch.float32), 2, dim=-1)
+    y1 = x1 * cos - x2 * sin
+    y2 = x2 * cos + x1 * sin
+    return torch.cat((y1, y2), dim=-1).to(x.dtype)
+
+
+def rotary_forward(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor, cos_sin_cache: torch.Tensor):
+    """RotaryEmbedding.forward (layers/rotary_embedding.py:37-48): the table row of each token's position,
+    broadcast over heads, applied to q [T, Hq, D] and k [T, Hkv, D]."""
+    cos_sin = cos_sin_cache[positions]  # [T, 1, D]
+    cos, sin = cos_sin.chunk(2, dim=-1)
+    return apply_rotary_emb(q, cos, sin), apply_rotary_emb(k, cos, sin)
+
+
+def store_kvcache(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor) -> None:
+    """Paged KV write (layers/attention.py:11-41), in place: for each token t with slot s = slot_mapping[t] != -1,
+    the whole [Hkv, D] row of k[t] / v[t] goes to slot s of the caches [blocks, block_size, Hkv, D]
+    (flat slot index s = block * block_size + offset). Rows of tokens with slot -1 are not written."""
+    hkv, d = k.shape[1], k.shape[2]
+    keep = slot_mapping != -1
+    slots = slot_mapping[keep].long()
+    k_cache.view(-1, hkv, d)[slots] = k[keep]
+    v_cache.view(-1, hkv, d)[slots] = v[keep]
+
+
+def qk_norm_rope_kv(q, k, v, positions, q_weight, k_weight, eps, cos_sin_cache, k_cache, v_cache, slot_mapping,
+                    write_k):
+    """The unfused pre-attention composition (models/qwen3.py:89-105 then layers/attention.py:64-76):
+    q_norm and k_norm (rms_forward per head row), rotary_emb, then store_kvcache of the rotated k and raw v.
+    Mutates the caches (unless they are empty); returns (q_out [T, Hq, D] contiguous, k_out or None)."""
+    qn = rms_forward(q, q_weight, eps)
+    kn = rms_forward(k, k_weight, eps)
+    q_out, k_rot = rotary_forward(positions, qn, kn, cos_sin_cache)
+    if k_cache.numel() > 0:
+        store_kvcache(k_rot, v, k_cache, v_cache, slot_mapping)
+    return q_out.contiguous(), (k_rot.contiguous() if write_k else None)
+
+
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """SiluAndMul (layers/activation.py:15-18): gate, up = halves of the last dim; silu(gate) in fp32 rounded to
+    x's dtype, times up (a bf16 product)."""
+    gate, up = x.chunk(2, -1)
+    return torch.nn.functional.silu(gate) * up
+
+
+def matmul_fp64(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """The GEMM reference of tests/test_kernels_matmul.py:52: exact-ish float64 product of the inputs."""
+    return a.double() @ b.double()

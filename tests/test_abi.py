@@ -1,0 +1,90 @@
+"""The C-ABI library (CPU only, no kernel launches): libnvhip.so loads, exports every function include/nvhip.h
+declares with the argument count the Python binding uses, and rejects bad arguments before launching anything
+(those paths return before any HIP call, so they run without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from nanovllm_hip import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nvhip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?\w+\s*\*?\s*(nvhip_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return out
+
+
+def test_header_declares_the_five_kernels():
+    names = set(declared_functions())
+    assert {"nvhip_qk_norm_rope_kv_bf16", "nvhip_rms_norm_bf16", "nvhip_add_rms_norm_bf16", "nvhip_silu_mul_bf16",
+            "nvhip_matmul", "nvhip_last_error", "nvhip_abi_version"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    decl = declared_functions()
+    for name, nargs in decl.items():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no Python binding"
+        assert len(_lib.SIGNATURES[name]) == nargs, f"{name}: header has {nargs} args"
+    assert set(_lib.SIGNATURES) == set(decl)
+    assert lib.nvhip_abi_version() == _lib.ABI_VERSION
+
+
+def _err():
+    return _lib.lib().nvhip_last_error().decode()
+
+
+def test_qk_rejects_bad_arguments_without_launching():
+    f = _lib.lib().nvhip_qk_norm_rope_kv_bf16
+    P = None
+    common = dict(q_stride=4096, k_stride=4096, v_stride=4096, cs_stride=128, max_pos=40960, num_slots=0)
+
+    def call(T=4, Hq=16, Hkv=8, D=128, k_cache=None, v_cache=None, slot=None, q_stride=4096):
+        return f(P, P, P, P, P, q_stride, common["k_stride"], common["v_stride"], P, slot, P, P, P,
+                 common["cs_stride"], common["max_pos"], k_cache, v_cache, 16, T, Hq, Hkv, D, 1e-6, P)
+
+    assert call(D=96) == _lib.NVHIP_EINVAL and "head_dim" in _err()
+    assert call(Hq=12, Hkv=8) == _lib.NVHIP_EINVAL and "multiple" in _err()
+    assert call(T=-1) == _lib.NVHIP_EINVAL
+    assert call(k_cache=ctypes.c_void_p(16)) == _lib.NVHIP_EINVAL and "together" in _err()
+    assert call(T=0) == _lib.NVHIP_OK and _err() == ""  # T = 0: nothing to do, nothing launched
+    assert call() == _lib.NVHIP_EINVAL and "null" in _err()
+
+
+def test_norm_silu_matmul_reject_bad_arguments_without_launching():
+    lib = _lib.lib()
+    assert lib.nvhip_rms_norm_bf16(None, None, None, 4, 1, 1024, 0, 0, 1e-6, None) == _lib.NVHIP_EINVAL
+    assert lib.nvhip_rms_norm_bf16(None, None, None, 0, 1, 1024, 0, 1024, 1e-6, None) == _lib.NVHIP_OK
+    assert lib.nvhip_rms_norm_bf16(None, None, None, 4, 1, 1024, 0, 1024, 1e-6, None) == _lib.NVHIP_EINVAL
+    assert "null" in _err()
+    assert lib.nvhip_add_rms_norm_bf16(None, None, None, None, None, 4, 512, 1024, 1024, 1e-6, None) == \
+        _lib.NVHIP_EINVAL and "stride" in _err()
+    assert lib.nvhip_add_rms_norm_bf16(None, None, None, None, None, 0, 1024, 1024, 1024, 1e-6, None) == _lib.NVHIP_OK
+    assert lib.nvhip_silu_mul_bf16(None, None, 4, 100, 64, None) == _lib.NVHIP_EINVAL
+    assert lib.nvhip_silu_mul_bf16(None, None, 0, 128, 64, None) == _lib.NVHIP_OK
+    m = lib.nvhip_matmul
+    assert m(None, None, None, 4, 4, 4, 4, 1, 4, 1, 4, 1, 7, 0, None) == _lib.NVHIP_EINVAL and "dtype" in _err()
+    assert m(None, None, None, 4, 4, 4, 4, 1, 4, 1, 4, 1, 0, 5, None) == _lib.NVHIP_EINVAL and "precision" in _err()
+    assert m(None, None, None, 4, 4, 4, -4, 1, 4, 1, 4, 1, 0, 0, None) == _lib.NVHIP_EINVAL
+    assert m(None, None, None, 0, 4, 4, 4, 1, 4, 1, 4, 1, 1, 0, None) == _lib.NVHIP_OK
+    assert m(None, None, None, 4, 4, 4, 4, 1, 4, 1, 4, 1, 1, 0, None) == _lib.NVHIP_EINVAL and "null" in _err()
+
+
+def test_check_maps_status_to_exceptions():
+    lib = _lib.lib()
+    lib.nvhip_silu_mul_bf16(None, None, 4, 100, 64, None)
+    with pytest.raises(ValueError, match="stride"):
+        _lib.check(_lib.NVHIP_EINVAL, "silu")
+    with pytest.raises(_lib.KernelError):
+        _lib.check(_lib.NVHIP_ELAUNCH, "silu")
+    _lib.check(_lib.NVHIP_OK, "silu")

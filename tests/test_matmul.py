@@ -1,0 +1,115 @@
+"""GPU parity of the GEMM (nvhip_matmul) against float64.
+
+The reference's tests/test_kernels_matmul.py: torch.testing.assert_close(C, A.double() @ B.double()) with
+  fp32 "ieee": rtol 1e-4,   atol 1e-4 * sqrt(K)
+  fp32 "tf32": rtol 1e-2,   atol 1e-2 * sqrt(K)
+  bf16:        rtol 1.6e-2, atol 1e-2 * sqrt(K)
+over its shape grid (M = 1 decode rows, sizes that are not multiples of any tile, K < one K-tile) for B row-major
+and B = W.t() of an nn.Linear weight, plus the guard that "ieee" is not silently tf32. Added: the Qwen3-0.6B
+projection shapes at M = 32 and 2048 (bf16, B = W.t(), A ~N(0,1)/sqrt(K)), fp32 4096^3, strided/offset views and
+the committed golden products.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from nanovllm_hip.kernels import matmul
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {
+    ("fp32", "ieee"): (1e-4, 1e-4),
+    ("fp32", "tf32"): (1e-2, 1e-2),
+    ("bf16", "ieee"): (1.6e-2, 1e-2),
+}
+DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16}
+SHAPES = [(1, 1024, 4096), (1, 3072, 1024), (7, 33, 65), (17, 129, 257), (100, 300, 70), (127, 255, 1000),
+          (512, 512, 512), (1000, 1000, 1000), (3, 5, 2)]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "matmul_small.npz")
+
+
+def check(a, b, prec, rtol_atol):
+    c = matmul(a, b, input_precision=prec)
+    assert c.shape == (a.shape[0], b.shape[1]) and c.dtype == a.dtype
+    ref = oracle.matmul_fp64(a.cpu(), b.cpu())
+    rtol, atol = rtol_atol
+    torch.testing.assert_close(c.cpu().double(), ref, rtol=rtol, atol=atol * math.sqrt(max(a.shape[1], 1)))
+
+
+@pytest.mark.parametrize("b_transposed", [False, True])
+@pytest.mark.parametrize("dtype,prec", list(TOL))
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_matmul(M, N, K, dtype, prec, b_transposed):
+    g = torch.Generator("cpu").manual_seed(0)
+    a = torch.randn(M, K, generator=g).to(DTYPES[dtype]).to(DEV)
+    if b_transposed:
+        b = torch.randn(N, K, generator=g).to(DTYPES[dtype]).to(DEV).t()
+    else:
+        b = torch.randn(K, N, generator=g).to(DTYPES[dtype]).to(DEV)
+    check(a, b, prec, TOL[(dtype, prec)])
+
+
+def test_ieee_is_not_tf32():
+    g = torch.Generator("cpu").manual_seed(0)
+    a = torch.randn(256, 4096, generator=g).to(DEV)
+    b = torch.randn(4096, 256, generator=g).to(DEV)
+    ref = oracle.matmul_fp64(a.cpu(), b.cpu())
+    err_ieee = (matmul(a, b, "ieee").cpu().double() - ref).abs().max().item()
+    err_tf32 = (matmul(a, b, "tf32").cpu().double() - ref).abs().max().item()
+    assert err_ieee < 1e-2 < err_tf32, (err_ieee, err_tf32)
+
+
+QWEN_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}
+
+
+@pytest.mark.parametrize("M", [32, 2048])
+@pytest.mark.parametrize("layer", list(QWEN_SHAPES))
+def test_qwen_projection_shapes(layer, M):
+    K, N = QWEN_SHAPES[layer]
+    g = torch.Generator("cpu").manual_seed(M + K + N)
+    a = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    c = matmul(a, w.t())
+    ref = oracle.matmul_fp64(a.cpu(), w.cpu().t())
+    # |C| ~ 1 here (A is scaled by 1/sqrt(K)): the bf16 tolerance with atol 1e-2
+    torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
+
+
+def test_fp32_4096_cube():
+    g = torch.Generator("cpu").manual_seed(4096)
+    a = torch.randn(4096, 4096, generator=g).to(DEV)
+    b = torch.randn(4096, 4096, generator=g).to(DEV)
+    c = matmul(a, b, "ieee")
+    # float64 reference on the GPU (a 4096^3 float64 product is minutes on the CPU)
+    ref = a.double() @ b.double()
+    torch.testing.assert_close(c.double(), ref, rtol=1e-4, atol=1e-4 * 64)
+
+
+def test_strided_views_and_empty():
+    g = torch.Generator("cpu").manual_seed(5)
+    big_a = torch.randn(70, 300, generator=g).to(torch.bfloat16).to(DEV)
+    big_b = torch.randn(300, 310, generator=g).to(torch.bfloat16).to(DEV)
+    check(big_a[3:60, 7:263], big_b[:256, 9:130], "ieee", TOL[("bf16", "ieee")])  # offset views, odd strides
+    check(big_a[::2, :128], big_b[10:138, ::2], "ieee", TOL[("bf16", "ieee")])  # non-unit strides
+    check(big_a.float()[:, :64], big_b.float()[:64, :33].t().contiguous().t(), "ieee", TOL[("fp32", "ieee")])
+    z = matmul(big_a[:, :0], big_b[:0, :5])
+    assert z.shape == (70, 5) and not z.any()
+    assert matmul(big_a[:0], big_b[:300, :5]).shape == (0, 5)
+
+
+def test_golden_small():
+    z = np.load(GOLDEN)
+    for (M, N, K) in ((7, 33, 65), (20, 40, 300)):
+        a = torch.from_numpy(z[f"a_f32_{M}_{N}_{K}"]).to(DEV)
+        w = torch.from_numpy(z[f"w_f32_{M}_{N}_{K}"]).to(DEV)
+        ref = torch.from_numpy(z[f"c_f64_{M}_{N}_{K}"])
+        torch.testing.assert_close(matmul(a, w.t()).cpu().double(), ref, rtol=1e-4, atol=1e-4 * math.sqrt(K))
+        ab = torch.from_numpy(z[f"a_bf16_{M}_{N}_{K}"].astype(np.int16)).view(torch.bfloat16).to(DEV)
+        wb = torch.from_numpy(z[f"w_bf16_{M}_{N}_{K}"].astype(np.int16)).view(torch.bfloat16).to(DEV)
+        refb = torch.from_numpy(z[f"cb_f64_{M}_{N}_{K}"])
+        torch.testing.assert_close(matmul(ab, wb.t()).cpu().double(), refb, rtol=1.6e-2, atol=1e-2 * math.sqrt(K))

@@ -1,0 +1,187 @@
+"""GPU parity of RMSNorm, Add+RMSNorm and SiLU x Mul (nvhip_rms_norm_bf16, nvhip_add_rms_norm_bf16,
+nvhip_silu_mul_bf16) against the CPU oracle.
+
+Structure of the reference's tests/test_kernels_norm_act.py: every output within MAX_ULP = 2 bf16 ulps of the
+oracle (only the fp32 summation order of the mean of squares differs, which can move the normalised value across
+one bf16 rounding boundary, two after the weight multiply); the new residual of Add+RMSNorm has no reduction and
+must be bitwise equal. SiLU x Mul has no reduction either: it is bitwise equal to torch's own GPU silu (the oracle
+run on the GPU, which is what the reference's test compares against) and within 1 ulp of the CPU oracle, whose
+vectorised exp may differ from the device exp in the last fp32 bit.
+Cases: the reference's grid (rows 1/7/128/4097 x n 128/1024, strided q/k views, SiLU at 3072) plus the MI355X
+workload (T 1/32/2048/8192 at hidden 1024 and gate_up 2 x 3072) and shapes that take the fallback kernels.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import EPS, HEAD_DIM, HIDDEN, INTERMEDIATE, KV_HEADS, Q_HEADS, bf16_randn, max_ulp, norm_weight
+from nanovllm_hip.kernels import fused_add_rms_norm, fused_add_rms_norm_, rms_norm, silu_and_mul
+
+pytestmark = pytest.mark.gpu
+
+MAX_ULP = 2
+DEV = "cuda"
+ROWS = [1, 7, 128, 4097]
+WORKLOAD_T = [1, 32, 2048, 8192]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "norm_act_t16.npz")
+
+
+def check_rms(x, w):
+    y = rms_norm(x.to(DEV), w.to(DEV), EPS)
+    ref = oracle.rms_forward(x, w, EPS)
+    assert y.shape == ref.shape and y.dtype == torch.bfloat16
+    assert max_ulp(y, ref) <= MAX_ULP
+
+
+def check_add(x, r, w):
+    y, s = fused_add_rms_norm(x.to(DEV), r.to(DEV), w.to(DEV), EPS)
+    y_ref, s_ref = oracle.add_rms_forward(x, r, w, EPS)
+    assert max_ulp(y, y_ref) <= MAX_ULP
+    assert torch.equal(s.cpu(), s_ref), "new residual must be bitwise"
+    # in-place variant: same outputs, residual overwritten
+    r_dev = r.to(DEV)
+    y2, r2 = fused_add_rms_norm_(x.to(DEV), r_dev, w.to(DEV), EPS)
+    assert r2.data_ptr() == r_dev.data_ptr()
+    assert torch.equal(y2, y) and torch.equal(r_dev, s)
+
+
+def check_silu(x):
+    xd = x.to(DEV)
+    out = silu_and_mul(xd)
+    assert torch.equal(out, oracle.silu_and_mul(xd)), "not bitwise vs torch's GPU silu"
+    assert max_ulp(out, oracle.silu_and_mul(x)) <= 1
+
+
+@pytest.mark.parametrize("n", [HEAD_DIM, HIDDEN])
+@pytest.mark.parametrize("rows", ROWS)
+def test_rms_norm(rows, n):
+    g = torch.Generator("cpu").manual_seed(rows * 7 + n)
+    check_rms(bf16_randn((rows, n), g), norm_weight(n, g))
+
+
+@pytest.mark.parametrize("tokens", ROWS)
+def test_qk_norm_strided_views(tokens):
+    g = torch.Generator("cpu").manual_seed(tokens * 3 + 1)
+    w = norm_weight(HEAD_DIM, g)
+    qkv = bf16_randn((tokens, (Q_HEADS + 2 * KV_HEADS) * HEAD_DIM), g)
+    q, k, _ = qkv.split([Q_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM], dim=-1)
+    qd, kd, _ = qkv.to(DEV).split([Q_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM], dim=-1)
+    for cpu, dev, h in ((q, qd, Q_HEADS), (k, kd, KV_HEADS)):
+        y = rms_norm(dev.view(-1, h, HEAD_DIM), w.to(DEV), EPS)
+        ref = oracle.rms_forward(cpu.view(-1, h, HEAD_DIM), w, EPS)
+        assert max_ulp(y, ref) <= MAX_ULP
+
+
+@pytest.mark.parametrize("n", [HEAD_DIM, HIDDEN])
+@pytest.mark.parametrize("rows", ROWS)
+def test_add_rms_norm(rows, n):
+    g = torch.Generator("cpu").manual_seed(rows * 5 + n)
+    check_add(bf16_randn((rows, n), g), bf16_randn((rows, n), g), norm_weight(n, g))
+
+
+@pytest.mark.parametrize("rows", ROWS)
+def test_silu_and_mul(rows):
+    g = torch.Generator("cpu").manual_seed(rows)
+    check_silu(bf16_randn((rows, 2 * INTERMEDIATE), g))
+
+
+@pytest.mark.parametrize("tokens", WORKLOAD_T)
+def test_workload(tokens):
+    g = torch.Generator("cpu").manual_seed(1000 + tokens)
+    w = norm_weight(HIDDEN, g)
+    x, r = bf16_randn((tokens, HIDDEN), g), bf16_randn((tokens, HIDDEN), g)
+    check_rms(x, w)
+    check_add(x, r, w)
+    check_silu(bf16_randn((tokens, 2 * INTERMEDIATE), g))
+
+
+def test_golden_t16():
+    z = np.load(GOLDEN)
+    u16 = lambda name: torch.from_numpy(z[name].astype(np.int16)).view(torch.bfloat16)
+    for n in (1024, 128):
+        x, r, w = u16(f"x_{n}").to(DEV), u16(f"r_{n}").to(DEV), u16(f"w_{n}").to(DEV)
+        assert max_ulp(rms_norm(x, w, EPS), u16(f"rms_{n}")) <= MAX_ULP
+        y, s = fused_add_rms_norm(x, r, w, EPS)
+        assert max_ulp(y, u16(f"add_y_{n}")) <= MAX_ULP
+        assert torch.equal(s.cpu(), u16(f"add_res_{n}"))
+    assert max_ulp(silu_and_mul(u16("gate_up").to(DEV)), u16("silu")) <= 1
+
+
+@pytest.mark.parametrize("n", [100, 1000, 3000, 40, 2560, 8192])
+def test_other_widths(n):
+    # 100/1000/3000/40 take the block-per-row fallback (n % 8 != 0 or n/8 without a register kernel),
+    # 2560 and 8192 register-resident kernels with 5 and 16 vectors per lane
+    g = torch.Generator("cpu").manual_seed(n)
+    rows = 33
+    w = norm_weight(n, g)
+    x, r = bf16_randn((rows, n), g), bf16_randn((rows, n), g)
+    check_rms(x, w)
+    check_add(x, r, w)
+    check_silu(bf16_randn((rows, 2 * n), g))
+
+
+def test_strided_rows_and_unaligned():
+    g = torch.Generator("cpu").manual_seed(77)
+    n = HIDDEN
+    w = norm_weight(n, g)
+    big = bf16_randn((50, n + 72), g)
+    check_rms(big[:, :n], w)  # padded row stride, aligned
+    check_rms(big[:, 1:n + 1], w)  # 2-byte offset: fallback path
+    r = bf16_randn((50, n + 24), g)
+    check_add(big[:, 8:n + 8], r[:, :n], w)
+    y, s = fused_add_rms_norm(big[:, 3:n + 3].to(DEV), r[:, 5:n + 5].to(DEV), w.to(DEV), EPS)
+    y_ref, s_ref = oracle.add_rms_forward(big[:, 3:n + 3], r[:, 5:n + 5], w, EPS)
+    assert max_ulp(y, y_ref) <= MAX_ULP and torch.equal(s.cpu(), s_ref)
+    gu = bf16_randn((40, 2 * INTERMEDIATE + 16), g)
+    check_silu(gu[:, :2 * INTERMEDIATE])
+    check_silu(gu[:, 3:3 + 2 * INTERMEDIATE])
+
+
+def test_zero_rows_and_shapes():
+    w = torch.ones(HIDDEN, dtype=torch.bfloat16, device=DEV)
+    x = torch.empty(0, HIDDEN, dtype=torch.bfloat16, device=DEV)
+    assert rms_norm(x, w, EPS).shape == (0, HIDDEN)
+    y, s = fused_add_rms_norm(x, x, w, EPS)
+    assert y.shape == s.shape == (0, HIDDEN)
+    assert silu_and_mul(torch.empty(0, 2 * INTERMEDIATE, dtype=torch.bfloat16, device=DEV)).shape == (0, INTERMEDIATE)
+    # 3-D input of silu and a 4-D input of rms_norm are flattened to rows, as the reference does
+    g = torch.Generator("cpu").manual_seed(3)
+    x3 = bf16_randn((2, 5, 2 * 64), g)
+    out = silu_and_mul(x3.to(DEV))
+    assert out.shape == (10, 64) and max_ulp(out, oracle.silu_and_mul(x3.reshape(10, 128))) <= 1
+    x4 = bf16_randn((2, 3, 4, 64), g)
+    w64 = norm_weight(64, g)
+    y4 = rms_norm(x4.to(DEV), w64.to(DEV), EPS)
+    assert y4.shape == (24, 64) and max_ulp(y4, oracle.rms_forward(x4.reshape(24, 64), w64, EPS)) <= MAX_ULP
+
+
+def test_graph_capture_replay():
+    g = torch.Generator("cpu").manual_seed(9)
+    x = bf16_randn((64, HIDDEN), g).to(DEV)
+    r = bf16_randn((64, HIDDEN), g).to(DEV)
+    gu = bf16_randn((64, 2 * INTERMEDIATE), g).to(DEV)
+    w = norm_weight(HIDDEN, g).to(DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        rms_norm(x, w, EPS), fused_add_rms_norm(x, r, w, EPS), silu_and_mul(gu)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y1 = rms_norm(x, w, EPS)
+        y2, s2 = fused_add_rms_norm(x, r, w, EPS)
+        y3 = silu_and_mul(gu)
+    for _ in range(4):
+        x.copy_(bf16_randn(x.shape, g))
+        r.copy_(bf16_randn(r.shape, g))
+        gu.copy_(bf16_randn(gu.shape, g))
+        graph.replay()
+        torch.cuda.synchronize()
+        e1 = rms_norm(x, w, EPS)
+        e2, es2 = fused_add_rms_norm(x, r, w, EPS)
+        e3 = silu_and_mul(gu)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, e1) and torch.equal(y2, e2) and torch.equal(s2, es2) and torch.equal(y3, e3)

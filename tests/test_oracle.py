@@ -1,0 +1,284 @@
+"""Pins the CPU oracle (oracle/torch_ref.py) independently of its own formulas (CPU only).
+
+The reference ships no golden vectors for this path, so each oracle function is checked against what the
+mathematics fixes, chosen so that a plausible slip (a dropped term, a wrong sign, a swapped half, a wrong index or
+divisor, a missing rounding, a transposed operand) fails at least one check:
+  rms_forward       hand-computed known answers; float64 closed form; float64 emulation of the rounding points;
+                    power-of-two scale invariance (eps = 0); eps visible on tiny rows
+  add_rms_forward   residual = exact float64 sum rounded once; y = RMSNorm of the *unrounded* sum; r = 0 reduces to
+                    rms_forward
+  rope table        float64 cos/sin of p / theta^(2i/D) at small p; layout [max_pos, 1, (cos | sin)]
+  apply_rotary_emb  identity table; complex multiplication (x1 + i x2) e^{i angle} in float64; norm preservation;
+                    dot products depend only on the position difference; hand-computed 90-degree rotation
+  store_kvcache     brute-force per-element loop with the flat slot formula block * block_size + offset
+  qk_norm_rope_kv   identity rotation reduces it to the norms; cache rows equal k_out / raw v; empty cache no-op
+  silu_and_mul      float64 closed form; known answers at 0 and large |g|; gate/up order
+  matmul_fp64       brute-force triple loop on the reference's tiny shapes
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+BF16 = torch.bfloat16
+
+
+def bits_f32_to_bf16_round(x32: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bf16 (ties to even), returned as float32. Independent of torch."""
+    u = np.ascontiguousarray(x32, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def f64(t: torch.Tensor) -> np.ndarray:
+    return t.to(torch.float64).numpy()
+
+
+def ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    def line(t):
+        i = t.contiguous().view(torch.int16).to(torch.int32)
+        return torch.where(i < 0, -(i & 0x7FFF), i)
+    return (line(a) - line(b)).abs()
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+def test_rms_known_answer():
+    # x = [3, 4, 0, 0], eps = 0: mean(x^2) = 25/4, x * rsqrt = [1.2, 1.6, 0, 0] -> bf16 [1.203125, 1.6015625, 0, 0]
+    # (a divisor of n-1 would give 1.039/1.386; a mean of |x| 1.714/2.286)
+    x = torch.tensor([[3.0, 4.0, 0.0, 0.0]], dtype=BF16)
+    y = oracle.rms_forward(x, torch.ones(4, dtype=BF16), 0.0)
+    assert y.tolist() == [[1.203125, 1.6015625, 0.0, 0.0]]
+    # weight 2 doubles exactly; a weight on one column touches only that column
+    y2 = oracle.rms_forward(x, torch.tensor([2.0, 1.0, 1.0, 1.0], dtype=BF16), 0.0)
+    assert y2.tolist() == [[2.40625, 1.6015625, 0.0, 0.0]]
+    # constant row: x * rsqrt(x^2 + eps) ~ 1 -> y = w; zero row stays 0 (eps keeps it finite)
+    w = torch.tensor([0.5, -1.25, 3.0, 1.0], dtype=BF16)
+    yc = oracle.rms_forward(torch.full((1, 4), 7.0, dtype=BF16), w, 1e-6)
+    assert torch.equal(yc[0], w)
+    assert torch.equal(oracle.rms_forward(torch.zeros(1, 4, dtype=BF16), w, 1e-6), torch.zeros(1, 4, dtype=BF16))
+
+
+@pytest.mark.parametrize("n", [128, 1024])
+def test_rms_closed_form_float64(n):
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(64, n, generator=g)
+    x[1] *= 1e-3  # mean(x^2) ~ 1e-6: eps = 1e-6 changes the result by ~sqrt(2), so a dropped eps fails
+    x[2] *= 300.0
+    x = x.to(BF16)
+    w = (1 + 0.1 * torch.randn(n, generator=g)).to(BF16)
+    eps = 1e-6
+    xd = f64(x)
+    y64 = xd / np.sqrt((xd ** 2).mean(axis=-1, keepdims=True) + eps) * f64(w)
+    y = oracle.rms_forward(x, w, eps)
+    ref = torch.from_numpy(bits_f32_to_bf16_round(y64.astype(np.float32))).to(BF16)
+    assert int(ulps(y, ref).max()) <= 2
+
+
+@pytest.mark.parametrize("n", [128, 1024])
+def test_rms_rounding_points(n):
+    """Float64 emulation of the rounding points: n = bf16(fp32(x * rstd)), y = bf16(fp32(n * w)). The float64 sum of
+    squares is order-free, so the torch oracle must agree bitwise on all but a few elements (a summation-order flip);
+    a missing rounding before the weight multiply would differ on a large fraction."""
+    g = torch.Generator().manual_seed(7 + n)
+    x = torch.randn(256, n, generator=g).to(BF16)
+    w = (1 + 0.1 * torch.randn(n, generator=g)).to(BF16)
+    eps = 1e-6
+    xd = f64(x)
+    mean = np.float32((xd ** 2).mean(axis=-1, keepdims=True))
+    rstd = (np.float32(1.0) / np.sqrt(mean + np.float32(eps), dtype=np.float32)).astype(np.float32)
+    normed = bits_f32_to_bf16_round((xd.astype(np.float32) * rstd).astype(np.float32))
+    y = bits_f32_to_bf16_round((normed * f64(w).astype(np.float32)).astype(np.float32))
+    got = oracle.rms_forward(x, w, eps).float().numpy()
+    assert np.mean(got == y) > 0.999
+    assert np.max(np.abs(got - y) / np.maximum(np.abs(y), 1e-30)) < 2 ** -6  # at most a couple of bf16 steps
+
+
+def test_rms_scale_invariance():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(32, 128, generator=g).to(BF16)
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(BF16)
+    y = oracle.rms_forward(x, w, 0.0)
+    for k in (-6, -1, 3, 9):
+        assert torch.equal(oracle.rms_forward(x * (2.0 ** k), w, 0.0), y)
+
+
+def test_rms_strided_3d_view_equals_rows():
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(5, 32 * 128, generator=g).to(BF16)
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(BF16)
+    q = qkv[:, :16 * 128].view(5, 16, 128)
+    assert torch.equal(oracle.rms_forward(q, w, 1e-6).reshape(80, 128),
+                       oracle.rms_forward(q.reshape(80, 128).contiguous(), w, 1e-6))
+
+
+# ------------------------------------------------------------------ Add + RMSNorm
+
+def test_add_rms_residual_and_unrounded_sum():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(128, 1024, generator=g).to(BF16)
+    r = torch.randn(128, 1024, generator=g).to(BF16)
+    w = (1 + 0.1 * torch.randn(1024, generator=g)).to(BF16)
+    y, res = oracle.add_rms_forward(x, r, w, 1e-6)
+    s64 = f64(x) + f64(r)  # exact: two bf16 values always sum exactly in float64
+    assert np.array_equal(res.float().numpy(), bits_f32_to_bf16_round(s64.astype(np.float32)))
+    y64 = s64 / np.sqrt((s64 ** 2).mean(axis=-1, keepdims=True) + 1e-6) * f64(w)
+    ref = torch.from_numpy(bits_f32_to_bf16_round(y64.astype(np.float32))).to(BF16)
+    assert int(ulps(y, ref).max()) <= 2
+    # normalising the rounded residual instead would be a different function: it must differ somewhere
+    assert not torch.equal(y, oracle.rms_forward(res, w, 1e-6))
+    # r = 0: plain RMSNorm, bitwise
+    y0, res0 = oracle.add_rms_forward(x, torch.zeros_like(x), w, 1e-6)
+    assert torch.equal(y0, oracle.rms_forward(x, w, 1e-6)) and torch.equal(res0, x)
+
+
+# ------------------------------------------------------------------ RoPE
+
+def test_rope_table_layout_and_values():
+    D, max_pos, base = 128, 40960, 1e6
+    cache = oracle.rope_cos_sin_cache(D, max_pos, base)
+    assert cache.shape == (max_pos, 1, D) and cache.dtype == torch.float32
+    p = np.arange(0, 17, dtype=np.float64)[:, None]
+    inv = base ** (-np.arange(0, D, 2, dtype=np.float64) / D)
+    ang = p * inv[None, :]
+    np.testing.assert_allclose(cache[:17, 0, :D // 2].double().numpy(), np.cos(ang), atol=5e-6)
+    np.testing.assert_allclose(cache[:17, 0, D // 2:].double().numpy(), np.sin(ang), atol=5e-6)
+    # row 0 is the identity rotation; frequency 0 turns by exactly one radian per position
+    assert torch.equal(cache[0, 0], torch.cat([torch.ones(D // 2), torch.zeros(D // 2)]))
+    np.testing.assert_allclose(cache[1000, 0, 0].item(), math.cos(1000.0), atol=1e-4)
+
+
+def test_rope_identity_and_known_rotation():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 4, 8, generator=g).to(BF16)
+    ones, zeros = torch.ones(4), torch.zeros(4)
+    assert torch.equal(oracle.apply_rotary_emb(x, ones, zeros), x)
+    # 90 degrees (cos 0, sin 1): (x1, x2) -> (-x2, x1)
+    y = oracle.apply_rotary_emb(x, zeros, ones)
+    assert torch.equal(y, torch.cat([-x[..., 4:], x[..., :4]], dim=-1))
+
+
+def test_rope_complex_form_and_invariants():
+    D = 128
+    cache = oracle.rope_cos_sin_cache(D, 40960, 1e6)
+    g = torch.Generator().manual_seed(8)
+    T = 64
+    q = torch.randn(T, 4, D, generator=g).to(BF16)
+    k = torch.randn(T, 4, D, generator=g).to(BF16)
+    pos = torch.randint(0, 40960, (T,), generator=g)
+    qr, kr = oracle.rotary_forward(pos, q, k, cache)
+    cs = cache[pos].double().numpy()  # [T, 1, D]
+    c, s = cs[..., :D // 2], cs[..., D // 2:]
+    z = f64(q)[..., :D // 2] + 1j * f64(q)[..., D // 2:]
+    zr = z * (c + 1j * s)
+    want = np.concatenate([zr.real, zr.imag], axis=-1)
+    got = f64(qr)
+    assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 1e-5)
+    # rotation keeps each (x1[i], x2[i]) pair's length
+    np.testing.assert_allclose(np.abs(zr), np.abs(f64(qr)[..., :D // 2] + 1j * f64(qr)[..., D // 2:]),
+                               rtol=2 ** -7, atol=1e-6)
+    # q.k after rotation depends only on the position difference
+    p1, p2 = torch.full((T,), 1000), torch.full((T,), 990)
+    a1, b1 = oracle.rotary_forward(p1, q, k, cache)
+    a2, b2 = oracle.rotary_forward(p1 + 3000, q, k, cache)
+    _, b3 = oracle.rotary_forward(p2 + 3000, q, k, cache)
+    _, b4 = oracle.rotary_forward(p2, q, k, cache)
+    d1 = (f64(a1) * f64(b4)).sum(-1)
+    d2 = (f64(a2) * f64(b3)).sum(-1)
+    np.testing.assert_allclose(d1, d2, atol=0.1 * np.sqrt(D))
+
+
+# ------------------------------------------------------------------ KV scatter
+
+def test_store_kvcache_brute_force():
+    g = torch.Generator().manual_seed(9)
+    T, blocks, bs, hkv, d = 6, 3, 4, 2, 4
+    k = torch.randn(T, hkv, d, generator=g).to(BF16)
+    v = torch.randn(T, hkv, d, generator=g).to(BF16)
+    slots = torch.tensor([5, -1, 0, 11, 7, -1], dtype=torch.int32)
+    kc = torch.randn(blocks, bs, hkv, d, generator=g).to(BF16)
+    vc = torch.randn(blocks, bs, hkv, d, generator=g).to(BF16)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    oracle.store_kvcache(k, v, kc, vc, slots)
+    flat_k, flat_v = kc_ref.view(-1), vc_ref.view(-1)
+    for t in range(T):
+        s = int(slots[t])
+        if s == -1:
+            continue
+        block, off = divmod(s, bs)
+        for h in range(hkv):
+            for i in range(d):
+                flat_k[((block * bs + off) * hkv + h) * d + i] = k[t, h, i]
+                flat_v[((block * bs + off) * hkv + h) * d + i] = v[t, h, i]
+    assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref)
+    assert torch.equal(kc[2, 3], k[3]) and torch.equal(vc[1, 1], v[0])  # slot 11 = block 2 offset 3; 5 = 1, 1
+
+
+def test_fused_composition():
+    g = torch.Generator().manual_seed(10)
+    T, Hq, Hkv, D = 9, 4, 2, 128
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g).to(BF16)
+    q, k, v = (t.view(T, -1, D) for t in qkv.split([Hq * D, Hkv * D, Hkv * D], dim=-1))
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    pos = torch.randint(0, 100, (T,), generator=g)
+    slots = torch.tensor([3, -1, 0, 7, 12, 5, -1, 9, 15], dtype=torch.int32)
+    cache = torch.randn(2, 4, 4, Hkv, D, generator=g).to(BF16)
+    kc, vc = cache[0].clone(), cache[1].clone()
+    table = oracle.rope_cos_sin_cache(D, 128, 1e6)
+    q_out, k_out = oracle.qk_norm_rope_kv(q, k, v, pos, qw, kw, 1e-6, table, kc, vc, slots, True)
+    # identity table: the outputs are the norms
+    ident = torch.cat([torch.ones(D // 2), torch.zeros(D // 2)]).view(1, 1, D)
+    qi, ki = oracle.qk_norm_rope_kv(q, k, v, torch.zeros_like(pos), qw, kw, 1e-6, ident, torch.empty(0),
+                                    torch.empty(0), None, True)
+    assert torch.equal(qi, oracle.rms_forward(q, qw, 1e-6)) and torch.equal(ki, oracle.rms_forward(k, kw, 1e-6))
+    # cache rows: rotated k and raw v at the named slots, the rest untouched
+    keep = slots >= 0
+    assert torch.equal(kc.view(-1, Hkv, D)[slots[keep].long()], k_out[keep])
+    assert torch.equal(vc.view(-1, Hkv, D)[slots[keep].long()], v[keep])
+    untouched = torch.ones(16, dtype=torch.bool)
+    untouched[slots[keep].long()] = False
+    assert torch.equal(kc.view(-1, Hkv, D)[untouched], cache[0].view(-1, Hkv, D)[untouched])
+    # write_k False -> None; empty cache -> nothing stored
+    q2, k2 = oracle.qk_norm_rope_kv(q, k, v, pos, qw, kw, 1e-6, table, torch.empty(0), torch.empty(0), None, False)
+    assert k2 is None and torch.equal(q2, q_out)
+
+
+# ------------------------------------------------------------------ SiLU x Mul
+
+def test_silu_closed_form_and_known_answers():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(64, 2 * 3072, generator=g).to(BF16)
+    out = oracle.silu_and_mul(x)
+    gate, up = f64(x[:, :3072]), f64(x[:, 3072:])
+    silu32 = (gate / (1 + np.exp(-gate))).astype(np.float32)
+    want = bits_f32_to_bf16_round((bits_f32_to_bf16_round(silu32) * up.astype(np.float32)).astype(np.float32))
+    got = out.float().numpy()
+    assert np.mean(got == want) > 0.999
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 2 ** -6
+    kat = torch.tensor([[0.0, 20.0, -100.0, 1.0, 3.0, 0.5, 2.0, 1.0]], dtype=BF16)
+    y = oracle.silu_and_mul(kat)
+    assert y[0, 0].item() == 0.0  # silu(0) = 0
+    assert y[0, 1].item() == 10.0  # silu(20) = 20 in bf16, times 0.5
+    assert abs(y[0, 2].item()) < 1e-30  # silu(-100) ~ -4e-42
+    assert y[0, 3].item() == 0.73046875  # bf16(1/(1+e^-1) = 0.7310586) = 0.73046875, times 1
+    # gate | up order: swapping the halves changes the result
+    assert not torch.equal(oracle.silu_and_mul(torch.cat([x[:, 3072:], x[:, :3072]], 1)), out)
+
+
+# ------------------------------------------------------------------ GEMM reference
+
+@pytest.mark.parametrize("M,N,K", [(3, 5, 2), (7, 33, 65)])
+def test_matmul_fp64_brute_force(M, N, K):
+    g = torch.Generator().manual_seed(M * N * K)
+    a = torch.randn(M, K, generator=g)
+    b = torch.randn(N, K, generator=g).t()  # B = W.t(): a transposed operand
+    c = oracle.matmul_fp64(a, b).numpy()
+    al, bl = a.tolist(), b.tolist()
+    for i in range(M):
+        for j in range(N):
+            assert abs(c[i, j] - math.fsum(al[i][kk] * bl[kk][j] for kk in range(K))) < 1e-9
+    assert c.shape == (M, N)
