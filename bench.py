@@ -181,6 +181,38 @@ def extras(torch, oracle, kernels, dev, steps):
     return out
 
 
+def copy_ceiling(torch, dev, mib=1024, reps=20):
+    """Device copy (torch copy_) of `mib` MiB: the practical read+write bandwidth ceiling, in GB/s."""
+    n = mib * 2 ** 20 // 2
+    src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)
+
+
+def profile_run(torch, kernels, wl, steps):
+    for i in range(steps):
+        wl.call(i, kernels.qk_norm_rope_kv)
+    torch.cuda.synchronize()
+    n = 256 * 2 ** 20 // 4
+    src = torch.ones(n, dtype=torch.float32, device=wl.k_cache.device)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {steps} x qk_norm_rope_kv (T={wl.T}, {fused_bytes(wl.T, wl.n_valid)} algorithmic bytes each), "
+          f"5 x copy of {n * 4} bytes", flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -189,6 +221,10 @@ def main():
     p.add_argument("--tokens", type=int, default=8192)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="only the headline kernel")
+    p.add_argument("--profile", action="store_true",
+                   help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
+                        "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
+                        "byte counters; prints the launch list instead of the JSON line")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the kernel path has no collective; "
@@ -203,7 +239,11 @@ def main():
     dev = torch.device("cuda:0")
     T = args.tokens
     wl = FusedWorkload(T, dev, torch, oracle)
-    ms, steps_done = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, args.steps, args.warmup)
+    if args.profile:
+        profile_run(torch, kernels, wl, args.steps)
+        return
+    # 40 launches per graph (the NSETS sets in turn): graph-to-graph boundaries add a few us, amortised here
+    ms, steps_done = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), 40, args.steps, args.warmup)
     nbytes = fused_bytes(T, wl.n_valid)
     gbs = nbytes / (ms * 1e-3) / 1e9
     traffic = None
@@ -222,6 +262,7 @@ def main():
     }
     if not args.no_extra:
         result["extra"] = extras(torch, oracle, kernels, dev, args.steps)
+        result["extra"]["copy_ceiling_GB/s"] = copy_ceiling(torch, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, oracle, T)
     print(json.dumps(result), flush=True)
