@@ -7,8 +7,10 @@
 //
 // Kernels:
 //   gemm_mfma_nt   bf16, A and B both K-contiguous (sak == 1, sbk == 1; B = W.t() of a [N, K] weight):
-//                  32x32x16 bf16 MFMA, LDS-staged double-buffered tiles, GROUP_M-swizzled, XCD-aware tile order.
+//                  32x32x16 bf16 MFMA, register + LDS staged pipeline, GROUP_M-swizzled, XCD-aware tile order.
 //   gemm_generic   any dtype/strides/precision: 64x64 tile, 4x4 outputs per thread, fp32 FMA.
+#include <type_traits>
+
 #include "common.h"
 
 namespace nvhip {
@@ -99,27 +101,31 @@ __global__ __launch_bounds__(kBlock) void gemm_generic(const GemmArgs g) {
 
 
 // ------------------------------------------------------------------------------------------------------------
-// bf16 MFMA kernel (A and B K-contiguous, C row-major with unit column stride).
+// bf16 MFMA kernel (A and B K-contiguous with 16-byte aligned rows, C with unit column stride).
 //
-// Block tile BM x BN x 64, 256 threads = 4 waves in a WAVES_M x WAVES_N grid, each wave owning WM x WN outputs
-// as FM x FN tiles of v_mfma_f32_32x32x16_bf16. The MFMA is issued with the operands swapped (its "A" is the
-// B^T = W fragment, its "B" the A fragment), so a lane's 16 accumulators hold, for one output row m, four runs of
-// 4 consecutive columns: the epilogue stores 8 bytes per lane per run.
-//   lane l, accumulator r of tile (fm, fn):  m = fm*32 + l%32,  n = fn*32 + 8*(r/4) + 4*(l/32) + r%4
-// Operand fragments (verified on gfx950): lane l reads row l%32, k = 8*(l/32) .. +8 of the 16-wide k step.
+// Block tile BM x BN x 64 with WAVES_M x WAVES_N waves, each owning WM x WN outputs as FM x FN tiles of
+// v_mfma_f32_32x32x16_bf16, issued with the operands swapped (its "A" is the B^T = W fragment, its "B" the A
+// fragment), so that lane l's 16 accumulators of tile (fm, fn) hold output row m = fm*32 + l%32, columns
+// n = fn*32 + 8*(r/4) + 4*(l/32) + r%4. Operand fragments (verified on gfx950): lane l reads row l%32,
+// k = 8*(l/32) .. +8 of the 16-wide k step.
 //
-// LDS: A and B tiles [rows][64] bf16 (128 bytes a row, eight 16-byte chunks), chunk c of row r stored at chunk
-// position c ^ (r & 7) so that the 32 rows a fragment read touches spread over all banks. Two stages: the global
-// loads of k-tile kt+1 are in flight (in registers) while k-tile kt is multiplied, then written to the other
-// stage; one barrier per k-tile.
-//
-// Tile order: 1-D grid; the block id is first remapped so that consecutive ids run on the same XCD (the dispatcher
-// deals blocks round-robin over the 8 XCDs), then mapped through the GROUP_M swizzle of the reference
-// (matmul.py:50-57): tile-rows in groups of GROUP_M, column-major inside a group, so blocks that run together
-// share A rows and B columns in their XCD's L2.
-// Rows past M / columns past N are loaded clamped to the last row (and never stored); k past K loads as zero.
+// Data path per k-tile of 64:
+//   global -> VGPRs   16-byte loads, RS tiles in flight in registers (RS = 2 keeps ~64 KB per block in flight,
+//                     enough to cover the ~2000-cycle L2 latency measured at full load)
+//   VGPRs -> LDS      two LDS stages, [rows][64] bf16 per operand; 16-byte chunk c of row r stored at chunk
+//                     c ^ ((r >> 1) & 7): with gfx950's 64 four-byte banks the 16 rows a half-wave fragment read
+//                     touches land in 16 distinct 16-byte bank groups (conflict-free)
+//   LDS -> MFMA       fragments for the next 16-wide k step are read while the current step's MFMAs issue
+// One barrier per k-tile; the loop body is branch-free (a prefetch past the last tile re-reads it) so the
+// compiler's wait counts keep the younger register stage in flight.
+// Epilogue: accumulators -> bf16 -> LDS tile (row pitch BN + 8) -> 16-byte row-contiguous stores.
+// Tile order: the block id is remapped so consecutive ids share an XCD (blocks are dealt round-robin over the 8
+// XCDs), then mapped through the GROUP_M swizzle of the reference (matmul.py:50-57).
+// Rows past M / columns past N are loaded clamped to the last row and never stored. With KTAIL, chunks past K
+// load as zero (K a multiple of 8); otherwise K is a multiple of 64 * RS.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kGroupM = 8;
 constexpr int kBK = 64;
@@ -146,15 +152,18 @@ __device__ __forceinline__ void tile_coords(int pid, int M, int N, int BM, int B
   pid_n = (pid % in_group) / group_rows;
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N>
-__global__ __launch_bounds__(256) void gemm_mfma_nt(const MfmaArgs g) {
-  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  constexpr int FM = WM / 32, FN = WN / 32;
-  static_assert(WAVES_M * WAVES_N == 4 && FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
-  constexpr int A_CHUNKS = BM * 8 / 256, B_CHUNKS = BN * 8 / 256;  // 16-byte chunks per thread per k-tile
-  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kBK];
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const MfmaArgs g) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
+  static_assert(FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+  constexpr int AC = BM * 8 / NT, BC = BN * 8 / NT;  // 16-byte chunks per thread per k-tile
+  static_assert(AC >= 1 && BC >= 1 && AC * NT == BM * 8 && BC * NT == BN * 8, "tile too small for the block");
+  static_assert(RS == 1 || RS == 2, "register stages");
+  constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
+  constexpr int OUT_PITCH = BN + 8;
+  constexpr int LDS_ELEMS = (2 * STAGE > BM * OUT_PITCH) ? 2 * STAGE : BM * OUT_PITCH;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[LDS_ELEMS];
 
   int pid_m, pid_n;
   tile_coords(blockIdx.x, g.M, g.N, BM, BN, pid_m, pid_n);
@@ -162,38 +171,40 @@ __global__ __launch_bounds__(256) void gemm_mfma_nt(const MfmaArgs g) {
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-  // global -> register staging: thread tid loads chunks tid + 256*i (row = chunk / 8, k-chunk = chunk % 8)
-  const uint16_t* a_src[A_CHUNKS];
-  const uint16_t* b_src[B_CHUNKS];
-  int a_lds[A_CHUNKS], b_lds[B_CHUNKS], a_kc[A_CHUNKS], b_kc[B_CHUNKS];
+  // chunk c = tid + NT*i of a tile: row c/8, logical k-chunk c%8, LDS chunk (c%8) ^ ((row >> 1) & 7)
+  const uint16_t* a_src[AC];
+  const uint16_t* b_src[BC];
+  int a_dst[AC], b_dst[BC], a_k[AC], b_k[BC];
 #pragma unroll
-  for (int i = 0; i < A_CHUNKS; ++i) {
-    const int ch = tid + 256 * i, row = ch / 8, kc = ch % 8;
+  for (int i = 0; i < AC; ++i) {
+    const int c = tid + NT * i, row = c / 8, kc = c % 8;
     a_src[i] = g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + kc * 8;
-    a_lds[i] = row * kBK + ((kc ^ (row & 7)) * 8);
-    a_kc[i] = kc * 8;
+    a_dst[i] = row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
+    a_k[i] = kc * 8;
   }
 #pragma unroll
-  for (int i = 0; i < B_CHUNKS; ++i) {
-    const int ch = tid + 256 * i, row = ch / 8, kc = ch % 8;
+  for (int i = 0; i < BC; ++i) {
+    const int c = tid + NT * i, row = c / 8, kc = c % 8;
     b_src[i] = g.w + int64_t(min(n0 + row, g.N - 1)) * g.swn + kc * 8;
-    b_lds[i] = row * kBK + ((kc ^ (row & 7)) * 8);
-    b_kc[i] = kc * 8;
+    b_dst[i] = BM * kBK + row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
+    b_k[i] = kc * 8;
   }
-  u32x4 ra[A_CHUNKS], rb[B_CHUNKS];
-  auto load_tile = [&](int k0) {
+  u32x4 ra[RS][AC], rb[RS][BC];
+  auto gload = [&](int kt, int slot) {
+    const int k0 = kt * kBK;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i)
-      ra[i] = (k0 + a_kc[i] < g.K) ? *reinterpret_cast<const u32x4*>(a_src[i] + k0) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < AC; ++i)
+      ra[slot][i] = (!KTAIL || k0 + a_k[i] < g.K) ? *reinterpret_cast<const u32x4*>(a_src[i] + k0) : u32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i)
-      rb[i] = (k0 + b_kc[i] < g.K) ? *reinterpret_cast<const u32x4*>(b_src[i] + k0) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < BC; ++i)
+      rb[slot][i] = (!KTAIL || k0 + b_k[i] < g.K) ? *reinterpret_cast<const u32x4*>(b_src[i] + k0) : u32x4{0, 0, 0, 0};
   };
-  auto store_tile = [&](int buf) {
+  auto lstore = [&](int stage, int slot) {
+    uint16_t* st = smem + stage * STAGE;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<u32x4*>(&As[buf][a_lds[i]]) = ra[i];
+    for (int i = 0; i < AC; ++i) *reinterpret_cast<u32x4*>(st + a_dst[i]) = ra[slot][i];
 #pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) *reinterpret_cast<u32x4*>(&Bs[buf][b_lds[i]]) = rb[i];
+    for (int i = 0; i < BC; ++i) *reinterpret_cast<u32x4*>(st + b_dst[i]) = rb[slot][i];
   };
 
   f32x16_t acc[FM][FN];
@@ -202,73 +213,103 @@ __global__ __launch_bounds__(256) void gemm_mfma_nt(const MfmaArgs g) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x16_t{};
 
-  // fragment read offsets: row = base + l%32 (row & 7 == l & 7), chunk = 2*kk + l/32
-  const int frag_row = lane % 32, frag_half = lane / 32, swz = lane & 7;
+  const int frag_row = lane % 32, frag_half = lane / 32, swz = (frag_row >> 1) & 7;
   const int nk = (g.K + kBK - 1) / kBK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * kBK);
+  gload(0, 0);
+  lstore(0, 0);
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
+  for (int r = 0; r < RS; ++r) gload(min(1 + r, nk - 1), r);
+  __syncthreads();
+
+  auto step = [&](int kt, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const uint16_t* As = smem + (kt & 1) * STAGE;
+    const uint16_t* Bs = As + BM * kBK;
+    bf16x8_t af[2][FM], bfr[2][FN];
+    auto load_frags = [&](int kk, int fs) {
       const int chunk = ((2 * kk + frag_half) ^ swz) * 8;
-      bf16x8_t af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][(wm * WM + i * 32 + frag_row) * kBK + chunk]);
+        af[fs][i] = *reinterpret_cast<const bf16x8_t*>(&As[(wm * WM + i * 32 + frag_row) * kBK + chunk]);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][(wn * WN + j * 32 + frag_row) * kBK + chunk]);
+        bfr[fs][j] = *reinterpret_cast<const bf16x8_t*>(&Bs[(wn * WN + j * 32 + frag_row) * kBK + chunk]);
+    };
+    load_frags(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      if (kk + 1 < kBK / 16) load_frags(kk + 1, (kk + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk & 1][j], af[kk & 1][i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < nk) store_tile(buf ^ 1);
+    lstore((kt + 1) & 1, slot);                 // tile kt+1 into the other stage (never read after the last tile)
+    gload(min(kt + 1 + RS, nk - 1), slot);      // refill the register slot
     __syncthreads();
+  };
+  for (int kt = 0; kt < nk; kt += RS) {
+    step(kt, std::integral_constant<int, 0>{});
+    if constexpr (RS == 2) step(kt + 1, std::integral_constant<int, 1>{});  // nk % RS == 0 (checked on the host)
   }
 
-  // epilogue: lane holds row m, columns n .. n+3 for each run
+  // epilogue: accumulators -> bf16 tile in LDS -> coalesced 16-byte row stores
+  uint16_t* ot = smem;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WM + i * 32 + frag_row;
-    if (m >= g.M) continue;
-    uint16_t* crow = g.c + int64_t(m) * g.scm;
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int run = 0; run < 4; ++run) {
-        const int n = n0 + wn * WN + j * 32 + 8 * run + 4 * frag_half;
-        const float v0 = acc[i][j][4 * run], v1 = acc[i][j][4 * run + 1];
-        const float v2 = acc[i][j][4 * run + 2], v3 = acc[i][j][4 * run + 3];
-        if (n + 3 < g.N) {
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-        } else {
-          const float v[4] = {v0, v1, v2, v3};
-          for (int e = 0; e < 4 && n + e < g.N; ++e) crow[n + e] = f32_to_bf16(v[e]);
-        }
+        const int r = wm * WM + i * 32 + frag_row, col = wn * WN + j * 32 + 8 * run + 4 * frag_half;
+        *reinterpret_cast<u32x2*>(&ot[r * OUT_PITCH + col]) =
+            u32x2{pack_bf16x2(acc[i][j][4 * run], acc[i][j][4 * run + 1]),
+                  pack_bf16x2(acc[i][j][4 * run + 2], acc[i][j][4 * run + 3])};
       }
+  __syncthreads();
+  constexpr int CPR = BN / 8;  // 16-byte chunks per output row
+  for (int c = tid; c < BM * CPR; c += NT) {
+    const int r = c / CPR, cc = (c % CPR) * 8;
+    const int m = m0 + r, n = n0 + cc;
+    if (m >= g.M) continue;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(&ot[r * OUT_PITCH + cc]);
+    uint16_t* dst = g.c + int64_t(m) * g.scm + n;
+    if (n + 8 <= g.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else {
+      for (int e = 0; e < 8 && n + e < g.N; ++e) dst[e] = uint16_t(v[e / 2] >> (16 * (e & 1)));
+    }
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL>
 int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   const int64_t tiles = int64_t((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_mfma_nt<BM, BN, WAVES_M, WAVES_N>), dim3(unsigned(tiles)), dim3(256), 0, s, g);
+  if (tiles > INT32_MAX) return invalid("matmul: matrix too large");
+  hipLaunchKernelGGL((gemm_mfma_nt<BM, BN, WAVES_M, WAVES_N, RS, KTAIL>), dim3(unsigned(tiles)),
+                     dim3(WAVES_M * WAVES_N * 64), 0, s, g);
   return check_launch("matmul");
 }
 
-// Tile shape for an M x N output: enough tiles to fill the 256 CUs at the largest tile that allows it.
-int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
+// Tile shape by output size (measured on MI355X for the Qwen3-0.6B projections at M = 2048): 128x128 with 8 waves
+// when that gives >= 256 tiles, else 128x64 (N = 1024 projections), small-M tiles for decode batches.
+template <int RS, bool KTAIL>
+int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
-  if (g.M <= 32) return launch_mfma<32, 128, 1, 4>(g, s);
-  if (g.M <= 64) return launch_mfma<64, 128, 2, 2>(g, s);
-  if (tiles(256, 128) >= 256) return launch_mfma<256, 128, 2, 2>(g, s);
-  if (tiles(128, 128) >= 256) return launch_mfma<128, 128, 2, 2>(g, s);
-  return launch_mfma<128, 64, 2, 2>(g, s);
+  if (g.M <= 32) return launch_mfma<32, 64, 1, 2, RS, KTAIL>(g, s);
+  if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL>(g, s);
+  if (tiles(128, 128) >= 384) return launch_mfma<128, 128, 2, 4, RS, KTAIL>(g, s);
+  return launch_mfma<128, 64, 2, 2, RS, KTAIL>(g, s);
+}
+
+int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
+  const int nk = (g.K + kBK - 1) / kBK;
+  if (g.K % kBK != 0) return launch_mfma_shape<1, true>(g, s);
+  if (nk % 2 == 0) return launch_mfma_shape<2, false>(g, s);
+  return launch_mfma_shape<1, false>(g, s);
 }
 
 template <typename T, bool TF32>
@@ -299,7 +340,7 @@ extern "C" int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, in
   if (dtype == NVHIP_DTYPE_BF16) {
     // MFMA path: A and B K-contiguous with 16-byte aligned rows, C with unit column stride, sizes within int32
     const bool nt = sak == 1 && sbk == 1 && scn == 1 && K % 8 == 0 && K > 0 && sam % 8 == 0 && sbn % 8 == 0 &&
-                    aligned16(a) && aligned16(b) && (reinterpret_cast<uintptr_t>(c) & 7) == 0 && scm % 4 == 0 &&
+                    aligned16(a) && aligned16(b) &&
                     M < (int64_t(1) << 31) && N < (int64_t(1) << 31) && K < (int64_t(1) << 31);
     if (nt) {
       MfmaArgs m{static_cast<uint16_t*>(c), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
