@@ -35,6 +35,7 @@ HQ, HKV, D, MAX_POS, THETA, BLOCK, EPS = 16, 8, 128, 40960, 1e6, 256, 1e-6
 NUM_BLOCKS = 512
 PAD = 64
 NSETS = 4
+GEMM_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}  # (K, N)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qk_norm_rope_kv_t8192_traffic.json")
 
 
@@ -166,8 +167,7 @@ def extras(torch, oracle, kernels, dev, steps):
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     del xs, rs, gus
-    for layer, (K, N) in {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024),
-                          "o_proj": (2048, 1024)}.items():
+    for layer, (K, N) in GEMM_SHAPES.items():
         M = 2048
         a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
         wt = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
@@ -213,6 +213,18 @@ def profile_run(torch, kernels, wl, steps):
           f"5 x copy of {n * 4} bytes", flush=True)
 
 
+def profile_gemm(torch, kernels, dev, steps):
+    g = torch.Generator("cpu").manual_seed(3)
+    for layer, (K, N) in GEMM_SHAPES.items():
+        a = (torch.randn(2048, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+        w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
+        for _ in range(steps):
+            kernels.matmul(a, w.t())
+            torch.nn.functional.linear(a, w)
+        torch.cuda.synchronize()
+        print(f"profile: {steps} x matmul + F.linear, {layer} 2048x{N}x{K}", flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -221,6 +233,9 @@ def main():
     p.add_argument("--tokens", type=int, default=8192)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="only the headline kernel")
+    p.add_argument("--profile-gemm", action="store_true",
+                   help="for rocprofv3 counter runs: --steps eager launches of the bf16 GEMM at each Qwen3-0.6B "
+                        "projection shape (M = 2048), each followed by torch.nn.functional.linear on the same tensors")
     p.add_argument("--profile", action="store_true",
                    help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
                         "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
@@ -237,6 +252,9 @@ def main():
     import nanovllm_hip.kernels as kernels
 
     dev = torch.device("cuda:0")
+    if args.profile_gemm:
+        profile_gemm(torch, kernels, dev, args.steps)
+        return
     T = args.tokens
     wl = FusedWorkload(T, dev, torch, oracle)
     if args.profile:

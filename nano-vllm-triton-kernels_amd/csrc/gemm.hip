@@ -110,14 +110,15 @@ __global__ __launch_bounds__(kBlock) void gemm_generic(const GemmArgs g) {
 // k = 8*(l/32) .. +8 of the 16-wide k step.
 //
 // Data path per k-tile of 64:
-//   global -> VGPRs   16-byte loads, RS tiles in flight in registers (RS = 2 keeps ~64 KB per block in flight,
+//   global -> VGPRs   16-byte loads, RS tiles in flight in registers (RS = 2 keeps 48-96 KB per block in flight,
 //                     enough to cover the ~2000-cycle L2 latency measured at full load)
 //   VGPRs -> LDS      two LDS stages, [rows][64] bf16 per operand; 16-byte chunk c of row r stored at chunk
 //                     c ^ ((r >> 1) & 7): with gfx950's 64 four-byte banks the 16 rows a half-wave fragment read
 //                     touches land in 16 distinct 16-byte bank groups (conflict-free)
 //   LDS -> MFMA       fragments for the next 16-wide k step are read while the current step's MFMAs issue
-// One barrier per k-tile; the loop body is branch-free (a prefetch past the last tile re-reads it) so the
-// compiler's wait counts keep the younger register stage in flight.
+// The next k-tile's LDS writes and global loads are interleaved between the MFMAs (sched_group_barrier), and the
+// one barrier per k-tile sits before its last k step (see `step`). The loop body is branch-free (a prefetch past
+// the last tile re-reads it) so the compiler's wait counts keep the younger register stage in flight.
 // Epilogue: accumulators -> bf16 -> LDS tile (row pitch BN + 8) -> 16-byte row-contiguous stores.
 // Tile order: the block id is remapped so consecutive ids share an XCD (blocks are dealt round-robin over the 8
 // XCDs), then mapped through the GROUP_M swizzle of the reference (matmul.py:50-57).
@@ -157,12 +158,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
   static_assert(FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
-  constexpr int AC = BM * 8 / NT, BC = BN * 8 / NT;  // 16-byte chunks per thread per k-tile
+  constexpr int AC = BM * 8 / NT, BC = BN * 8 / NT, CH = AC + BC;  // 16-byte chunks per thread per k-tile
   static_assert(AC >= 1 && BC >= 1 && AC * NT == BM * 8 && BC * NT == BN * 8, "tile too small for the block");
   static_assert(RS == 1 || RS == 2, "register stages");
   constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
   constexpr int OUT_PITCH = BN + 8;
   constexpr int LDS_ELEMS = (2 * STAGE > BM * OUT_PITCH) ? 2 * STAGE : BM * OUT_PITCH;
+  constexpr int NMF = FM * FN;            // MFMAs per 16-wide k step
+  constexpr int WPK = (CH + 2) / 3;       // next-tile chunks written to LDS per k step (k steps 0..2)
+  constexpr int LPK = (CH + 3) / 4;       // chunks refilled from global memory per k step (k steps 0..3)
   __shared__ __attribute__((aligned(16))) uint16_t smem[LDS_ELEMS];
 
   int pid_m, pid_n;
@@ -171,42 +175,24 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-  // chunk c = tid + NT*i of a tile: row c/8, logical k-chunk c%8, LDS chunk (c%8) ^ ((row >> 1) & 7)
-  const uint16_t* a_src[AC];
-  const uint16_t* b_src[BC];
-  int a_dst[AC], b_dst[BC], a_k[AC], b_k[BC];
+  // chunk i < AC: A chunk c = tid + NT*i; else B chunk c = tid + NT*(i-AC). Row c/8, logical k-chunk c%8, stored
+  // in LDS at chunk (c%8) ^ ((row >> 1) & 7) of the row.
+  const uint16_t* src[CH];
+  int dst[CH], kofs[CH];
 #pragma unroll
-  for (int i = 0; i < AC; ++i) {
-    const int c = tid + NT * i, row = c / 8, kc = c % 8;
-    a_src[i] = g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + kc * 8;
-    a_dst[i] = row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
-    a_k[i] = kc * 8;
+  for (int i = 0; i < CH; ++i) {
+    const bool isA = i < AC;
+    const int c = tid + NT * (isA ? i : i - AC), row = c / 8, kc = c % 8;
+    src[i] = isA ? g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + kc * 8
+                 : g.w + int64_t(min(n0 + row, g.N - 1)) * g.swn + kc * 8;
+    dst[i] = (isA ? 0 : BM * kBK) + row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
+    kofs[i] = kc * 8;
   }
-#pragma unroll
-  for (int i = 0; i < BC; ++i) {
-    const int c = tid + NT * i, row = c / 8, kc = c % 8;
-    b_src[i] = g.w + int64_t(min(n0 + row, g.N - 1)) * g.swn + kc * 8;
-    b_dst[i] = BM * kBK + row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
-    b_k[i] = kc * 8;
-  }
-  u32x4 ra[RS][AC], rb[RS][BC];
-  auto gload = [&](int kt, int slot) {
-    const int k0 = kt * kBK;
-#pragma unroll
-    for (int i = 0; i < AC; ++i)
-      ra[slot][i] = (!KTAIL || k0 + a_k[i] < g.K) ? *reinterpret_cast<const u32x4*>(a_src[i] + k0) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < BC; ++i)
-      rb[slot][i] = (!KTAIL || k0 + b_k[i] < g.K) ? *reinterpret_cast<const u32x4*>(b_src[i] + k0) : u32x4{0, 0, 0, 0};
+  auto gload1 = [&](int i, int k0) -> u32x4 {
+    if (!KTAIL || k0 + kofs[i] < g.K) return *reinterpret_cast<const u32x4*>(src[i] + k0);
+    return u32x4{0, 0, 0, 0};
   };
-  auto lstore = [&](int stage, int slot) {
-    uint16_t* st = smem + stage * STAGE;
-#pragma unroll
-    for (int i = 0; i < AC; ++i) *reinterpret_cast<u32x4*>(st + a_dst[i]) = ra[slot][i];
-#pragma unroll
-    for (int i = 0; i < BC; ++i) *reinterpret_cast<u32x4*>(st + b_dst[i]) = rb[slot][i];
-  };
-
+  u32x4 r[RS][CH];
   f32x16_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -215,46 +201,74 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
 
   const int frag_row = lane % 32, frag_half = lane / 32, swz = (frag_row >> 1) & 7;
   const int nk = (g.K + kBK - 1) / kBK;
-  gload(0, 0);
-  lstore(0, 0);
+  // prologue: k-tile 0 -> LDS stage 0; k-tiles 1..RS in flight in the register slots
 #pragma unroll
-  for (int r = 0; r < RS; ++r) gload(min(1 + r, nk - 1), r);
+  for (int i = 0; i < CH; ++i) r[0][i] = gload1(i, 0);
+#pragma unroll
+  for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(smem + dst[i]) = r[0][i];
+#pragma unroll
+  for (int s = 0; s < RS; ++s)
+#pragma unroll
+    for (int i = 0; i < CH; ++i) r[s][i] = gload1(i, min(1 + s, nk - 1) * kBK);
   __syncthreads();
 
+  bf16x8_t af[2][FM], bfr[2][FN];
+  auto load_frags = [&](const uint16_t* st, int kk, int fs) {
+    const int chunk = ((2 * kk + frag_half) ^ swz) * 8;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[fs][i] = *reinterpret_cast<const bf16x8_t*>(&st[(wm * WM + i * 32 + frag_row) * kBK + chunk]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      bfr[fs][j] = *reinterpret_cast<const bf16x8_t*>(&st[BM * kBK + (wn * WN + j * 32 + frag_row) * kBK + chunk]);
+  };
+  load_frags(smem, 0, 0);
+
+  // One k-tile: four 16-wide k steps. In k step kk the wave reads the fragments of step kk+1, issues the MFMAs of
+  // step kk and, interleaved with them, writes a third of the next k-tile (from a register slot) into the other
+  // LDS stage and refills a quarter of that slot from global memory. The barrier sits before the last k step: by
+  // then the next stage is complete and every wave has read its last fragments of the current stage, so the first
+  // fragments of the next k-tile are read while the last MFMAs of this one issue.
   auto step = [&](int kt, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
-    const uint16_t* As = smem + (kt & 1) * STAGE;
-    const uint16_t* Bs = As + BM * kBK;
-    bf16x8_t af[2][FM], bfr[2][FN];
-    auto load_frags = [&](int kk, int fs) {
-      const int chunk = ((2 * kk + frag_half) ^ swz) * 8;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[fs][i] = *reinterpret_cast<const bf16x8_t*>(&As[(wm * WM + i * 32 + frag_row) * kBK + chunk]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bfr[fs][j] = *reinterpret_cast<const bf16x8_t*>(&Bs[(wn * WN + j * 32 + frag_row) * kBK + chunk]);
-    };
-    load_frags(0, 0);
+    const uint16_t* cur = smem + (kt & 1) * STAGE;
+    uint16_t* nxt = smem + ((kt + 1) & 1) * STAGE;
+    const int kload = min(kt + 1 + RS, nk - 1) * kBK;  // past the end: re-reads the last k-tile (never used)
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
-      if (kk + 1 < kBK / 16) load_frags(kk + 1, (kk + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);
+      if (kk + 1 < kBK / 16) {
+        load_frags(cur, kk + 1, (kk + 1) & 1);
+      } else {
+        __syncthreads();
+        load_frags(nxt, 0, 0);
+      }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk & 1][j], af[kk & 1][i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      if (kk < 3) {
+#pragma unroll
+        for (int c = kk * WPK; c < (kk + 1) * WPK && c < CH; ++c)
+          *reinterpret_cast<u32x4*>(nxt + dst[c]) = r[slot][c];
+      }
+#pragma unroll
+      for (int c = kk * LPK; c < (kk + 1) * LPK && c < CH; ++c) r[slot][c] = gload1(c, kload);
+      // issue order: fragment reads, then MFMAs with the LDS writes and the global loads between them
+      __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+#pragma unroll
+      for (int m = 0; m < NMF; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (kk < 3 && m < WPK) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        else if (m >= WPK && m < WPK + LPK) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
     }
-    lstore((kt + 1) & 1, slot);                 // tile kt+1 into the other stage (never read after the last tile)
-    gload(min(kt + 1 + RS, nk - 1), slot);      // refill the register slot
-    __syncthreads();
   };
   for (int kt = 0; kt < nk; kt += RS) {
     step(kt, std::integral_constant<int, 0>{});
     if constexpr (RS == 2) step(kt + 1, std::integral_constant<int, 1>{});  // nk % RS == 0 (checked on the host)
   }
+  __syncthreads();
 
   // epilogue: accumulators -> bf16 tile in LDS -> coalesced 16-byte row stores
   uint16_t* ot = smem;
@@ -264,23 +278,23 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int run = 0; run < 4; ++run) {
-        const int r = wm * WM + i * 32 + frag_row, col = wn * WN + j * 32 + 8 * run + 4 * frag_half;
-        *reinterpret_cast<u32x2*>(&ot[r * OUT_PITCH + col]) =
+        const int rr = wm * WM + i * 32 + frag_row, col = wn * WN + j * 32 + 8 * run + 4 * frag_half;
+        *reinterpret_cast<u32x2*>(&ot[rr * OUT_PITCH + col]) =
             u32x2{pack_bf16x2(acc[i][j][4 * run], acc[i][j][4 * run + 1]),
                   pack_bf16x2(acc[i][j][4 * run + 2], acc[i][j][4 * run + 3])};
       }
   __syncthreads();
   constexpr int CPR = BN / 8;  // 16-byte chunks per output row
   for (int c = tid; c < BM * CPR; c += NT) {
-    const int r = c / CPR, cc = (c % CPR) * 8;
-    const int m = m0 + r, n = n0 + cc;
+    const int rr = c / CPR, cc = (c % CPR) * 8;
+    const int m = m0 + rr, n = n0 + cc;
     if (m >= g.M) continue;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(&ot[r * OUT_PITCH + cc]);
-    uint16_t* dst = g.c + int64_t(m) * g.scm + n;
-    if (n + 8 <= g.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-      *reinterpret_cast<u32x4*>(dst) = v;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(&ot[rr * OUT_PITCH + cc]);
+    uint16_t* d = g.c + int64_t(m) * g.scm + n;
+    if (n + 8 <= g.N && (reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+      *reinterpret_cast<u32x4*>(d) = v;
     } else {
-      for (int e = 0; e < 8 && n + e < g.N; ++e) dst[e] = uint16_t(v[e / 2] >> (16 * (e & 1)));
+      for (int e = 0; e < 8 && n + e < g.N; ++e) d[e] = uint16_t(v[e / 2] >> (16 * (e & 1)));
     }
   }
 }
@@ -294,14 +308,16 @@ int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   return check_launch("matmul");
 }
 
-// Tile shape by output size (measured on MI355X for the Qwen3-0.6B projections at M = 2048): 128x128 with 8 waves
-// when that gives >= 256 tiles, else 128x64 (N = 1024 projections), small-M tiles for decode batches.
+// Tile shape by output size (measured on MI355X at the Qwen3-0.6B projections, M = 2048): the largest tile that
+// still gives >= 192 tiles (3/4 of the 256 CUs), small-M tiles for decode batches.
 template <int RS, bool KTAIL>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
   if (g.M <= 32) return launch_mfma<32, 64, 1, 2, RS, KTAIL>(g, s);
   if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL>(g, s);
-  if (tiles(128, 128) >= 384) return launch_mfma<128, 128, 2, 4, RS, KTAIL>(g, s);
+  if (tiles(256, 256) >= 192) return launch_mfma<256, 256, 4, 2, 1, KTAIL>(g, s);
+  if (tiles(128, 256) >= 192) return launch_mfma<128, 256, 2, 2, RS, KTAIL>(g, s);
+  if (tiles(128, 128) >= 192) return launch_mfma<128, 128, 2, 4, RS, KTAIL>(g, s);
   return launch_mfma<128, 64, 2, 2, RS, KTAIL>(g, s);
 }
 
