@@ -12,7 +12,8 @@ launch to launch so that the working set (> 256 MB) does not stay in the Infinit
 replayed from HIP graphs and timed with HIP events on the stream they run on.
 
 Also reported (under "extra"): the same kernel at T = 1, 32, 2048; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
-(hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048, in TFLOP/s.
+(hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
+and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM.
 The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
 sample of the same workload.
 
@@ -31,6 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = "qk-norm+RoPE+KV-write GB/s (%HBM peak) at T=8192; bf16 GEMM TFLOP/s"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 HQ, HKV, D, MAX_POS, THETA, BLOCK, EPS = 16, 8, 128, 40960, 1e6, 256, 1e-6
 NUM_BLOCKS = 512
 PAD = 64
@@ -178,6 +180,32 @@ def extras(torch, oracle, kernels, dev, steps):
         out[f"gemm_bf16_{layer}_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
                                            "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
                                            "torch_linear_us": round(ms_ref * 1e3, 2)}
+        del a, wt, b
+    # decode-sized GEMMs are weight-bandwidth bound: rotate over enough weight copies (>= 512 MiB) that every call
+    # reads its weight from HBM, as a decode step over 28 layers does
+    for layer, (K, N) in GEMM_SHAPES.items():
+        M = 32
+        nw = -(-(512 * 2 ** 20) // (N * K * 2))
+        a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+        w0 = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
+        ws = [w0.clone() for _ in range(nw)]
+        ms, _ = time_graph(torch, lambda i: kernels.matmul(a, ws[i].t()), nw, max(nw, steps), nw)
+        ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, ws[i]), nw, max(nw, steps), nw)
+        nbytes = 2 * (M * K + N * K + M * N)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"gemm_bf16_{layer}_M{M}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                         "torch_linear_us": round(ms_ref * 1e3, 2)}
+        del a, w0, ws
+    n = 4096
+    a = torch.randn(n, n, generator=g).to(dev)
+    b = torch.randn(n, n, generator=g).to(dev)
+    ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 1, 5, 2)
+    ms_ref, _ = time_graph(torch, lambda i: torch.matmul(a, b), 1, 5, 2)
+    tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    out["gemm_fp32_ieee_4096"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                  "frac_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4),
+                                  "torch_matmul_us": round(ms_ref * 1e3, 1)}
     return out
 
 
@@ -213,16 +241,19 @@ def profile_run(torch, kernels, wl, steps):
           f"5 x copy of {n * 4} bytes", flush=True)
 
 
-def profile_gemm(torch, kernels, dev, steps):
+def profile_gemm(torch, kernels, dev, steps, M):
     g = torch.Generator("cpu").manual_seed(3)
     for layer, (K, N) in GEMM_SHAPES.items():
-        a = (torch.randn(2048, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
-        w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
-        for _ in range(steps):
-            kernels.matmul(a, w.t())
-            torch.nn.functional.linear(a, w)
+        a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+        w0 = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
+        # small M is weight-bandwidth bound: rotate over >= 512 MiB of weight copies so each call reads from HBM
+        ws = [w0.clone() for _ in range(-(-(512 * 2 ** 20) // (N * K * 2)))] if M <= 64 else [w0]
+        for i in range(steps):
+            kernels.matmul(a, ws[i % len(ws)].t())
+            torch.nn.functional.linear(a, ws[i % len(ws)])
         torch.cuda.synchronize()
-        print(f"profile: {steps} x matmul + F.linear, {layer} 2048x{N}x{K}", flush=True)
+        print(f"profile: {steps} x matmul + F.linear, {layer} {M}x{N}x{K}, {len(ws)} weight copies", flush=True)
+        del ws, w0, a
 
 
 def main():
@@ -234,8 +265,9 @@ def main():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="only the headline kernel")
     p.add_argument("--profile-gemm", action="store_true",
-                   help="for rocprofv3 counter runs: --steps eager launches of the bf16 GEMM at each Qwen3-0.6B "
-                        "projection shape (M = 2048), each followed by torch.nn.functional.linear on the same tensors")
+                   help="for rocprofv3 runs: --steps eager launches of the bf16 GEMM at each Qwen3-0.6B projection "
+                        "shape (M = --gemm-m), each followed by torch.nn.functional.linear on the same tensors")
+    p.add_argument("--gemm-m", type=int, default=2048, help="M of the --profile-gemm products")
     p.add_argument("--profile", action="store_true",
                    help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
                         "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
@@ -253,7 +285,7 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.profile_gemm:
-        profile_gemm(torch, kernels, dev, args.steps)
+        profile_gemm(torch, kernels, dev, args.steps, args.gemm_m)
         return
     T = args.tokens
     wl = FusedWorkload(T, dev, torch, oracle)

@@ -8,6 +8,8 @@
 // Kernels:
 //   gemm_mfma_nt   bf16, A and B both K-contiguous (sak == 1, sbk == 1; B = W.t() of a [N, K] weight):
 //                  32x32x16 bf16 MFMA, register + LDS staged pipeline, GROUP_M-swizzled, XCD-aware tile order.
+//   gemm_skinny    bf16 with M <= 32, same layout: 16 columns per block, K split over 8 waves, 16x16x32 MFMA.
+//   gemm_mfma_f32  fp32, A K-contiguous, B K- or N-contiguous: 32x32x2 fp32 MFMA (exact products, fp32 sums).
 //   gemm_generic   any dtype/strides/precision: 64x64 tile, 4x4 outputs per thread, fp32 FMA.
 #include <type_traits>
 
@@ -127,6 +129,7 @@ __global__ __launch_bounds__(kBlock) void gemm_generic(const GemmArgs g) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGroupM = 8;
 constexpr int kBK = 64;
@@ -299,6 +302,188 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Skinny bf16 kernel for M <= 32 (decode batches), bound by reading W once: a block owns 16 output columns for all
+// M rows and its NW waves split K between them (wave w takes the 32-wide k steps w, w + NW, ..., so the block's
+// loads in flight cover NW consecutive steps of each W row). Each wave multiplies with v_mfma_f32_16x16x32_bf16
+// fed straight from global memory (lane l: row l % 16, k = 8 * (l / 16) .. +8 of the step, for both the A rows
+// and the W rows; W is read once, A is small and stays in L2), U steps of loads issued before their MFMAs. The
+// NW partial 16-row tiles are summed through LDS in wave order (deterministic), rounded to bf16 and stored.
+
+template <int MT, int NW, int U>
+__global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
+  __shared__ float red[NW][MT][4][64];
+  const int n0 = blockIdx.x * 16;
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int fr = lane % 16, fk = (lane / 16) * 8;
+  const uint16_t* wrow = g.w + int64_t(min(n0 + fr, g.N - 1)) * g.swn + fk;
+  const uint16_t* arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) arow[t] = g.a + int64_t(min(t * 16 + fr, g.M - 1)) * g.sam + fk;
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{};
+  const int nks = (g.K + 31) / 32;
+  for (int s0 = wave; s0 < nks; s0 += NW * U) {
+    bf16x8_t wf[U], af[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int ks = s0 + u * NW, k = ks * 32;
+      const bool in = ks < nks && k + fk < g.K;  // K % 8 == 0: a lane's 8 values are all in or all out
+      wf[u] = in ? *reinterpret_cast<const bf16x8_t*>(wrow + k) : bf16x8_t{};
+#pragma unroll
+      for (int t = 0; t < MT; ++t) af[u][t] = in ? *reinterpret_cast<const bf16x8_t*>(arow[t] + k) : bf16x8_t{};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[u][t], wf[u], acc[t], 0, 0, 0);
+  }
+  // lane l, register r of tile t holds C row t*16 + 4*(l/16) + r, column n0 + l%16
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < MT * 256; idx += NW * 64) {
+    const int t = idx / 256, r = (idx / 64) % 4, l = idx % 64;
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += red[w][t][r][l];
+    const int m = t * 16 + 4 * (l / 16) + r, n = n0 + l % 16;
+    if (m < g.M && n < g.N) g.c[int64_t(m) * g.scm + n] = f32_to_bf16(sum);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// fp32 MFMA kernel: v_mfma_f32_32x32x2_f32 forms exact fp32 products and accumulates them in fp32 (precision
+// "ieee"); with TF32 every input is first rounded to tf32. A is K-contiguous; B is either K-contiguous (W [N, K],
+// B = W.t()) or N-contiguous ([K, N]). 128x128 block tile, 4 waves of 64x64 (2x2 MFMA tiles, operands swapped as
+// in the bf16 kernel), k-tile 32. LDS holds both operands k-major ([k][m], [k][n]) with a row pitch of 160
+// floats, so the two half-waves of a fragment read (rows k and k+1, 32 consecutive floats each) hit disjoint bank
+// halves. Global loads are 16 bytes: 4 consecutive k of one row of A / W (8 lanes cover one row's 128 bytes), or
+// 4 consecutive n of one row of B. The next k-tile is loaded into registers while the current one is multiplied.
+struct F32Args {
+  float* c;
+  const float* a;
+  const float* b;
+  int M, N, K;
+  int64_t sam, sbk, sbn, scm;
+};
+
+template <bool B_NMAJOR, bool TF32>
+__global__ __launch_bounds__(256) void gemm_mfma_f32(const F32Args g) {
+  constexpr int BM = 128, BN = 128, BK = 32, P = 160, NT = 256;
+  constexpr int CH = BM * BK / 4 / NT;  // 16-byte chunks per thread per operand per k-tile (4)
+  __shared__ __attribute__((aligned(16))) float lds[2][2][BK * P];  // [stage][A | B][k * P + m]
+  int pid_m, pid_n;
+  tile_coords(blockIdx.x, g.M, g.N, BM, BN, pid_m, pid_n);
+  const int m0 = pid_m * BM, n0 = pid_n * BN;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int wm = wave / 2, wn = wave % 2;
+
+  // K-major chunks (A, and B when K-contiguous): chunk c covers row c / 8, k = 4 * (c % 8) .. +4
+  const float* asrc[CH];
+  const float* bsrc[CH];
+  int arow[CH], akc[CH], brow[CH], bkc[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + NT * i;
+    arow[i] = c / 8;
+    akc[i] = 4 * (c % 8);
+    asrc[i] = g.a + int64_t(min(m0 + arow[i], g.M - 1)) * g.sam + akc[i];
+    if constexpr (B_NMAJOR) {  // chunk c covers k row c / 32, n = 4 * (c % 32) .. +4 (clamped inside N)
+      brow[i] = c / 32;
+      bkc[i] = 4 * (c % 32);
+      bsrc[i] = g.b + min(n0 + bkc[i], g.N - 4);
+    } else {
+      brow[i] = c / 8;
+      bkc[i] = 4 * (c % 8);
+      bsrc[i] = g.b + int64_t(min(n0 + brow[i], g.N - 1)) * g.sbn + bkc[i];
+    }
+  }
+  f32x4_t ra[CH], rb[CH];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      ra[i] = (k0 + akc[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(asrc[i] + k0) : f32x4_t{0, 0, 0, 0};
+      if constexpr (B_NMAJOR)
+        rb[i] = (k0 + brow[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(bsrc[i] + int64_t(k0 + brow[i]) * g.sbk)
+                                     : f32x4_t{0, 0, 0, 0};
+      else
+        rb[i] = (k0 + bkc[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(bsrc[i] + k0) : f32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto tf = [](float x) { return TF32 ? round_tf32(x) : x; };
+  auto lstore = [&](int st) {
+    float* la = lds[st][0];
+    float* lb = lds[st][1];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) la[(akc[i] + e) * P + arow[i]] = tf(ra[i][e]);
+      if constexpr (B_NMAJOR) {
+        *reinterpret_cast<f32x4_t*>(&lb[brow[i] * P + bkc[i]]) =
+            f32x4_t{tf(rb[i][0]), tf(rb[i][1]), tf(rb[i][2]), tf(rb[i][3])};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lb[(bkc[i] + e) * P + brow[i]] = tf(rb[i][e]);
+      }
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+  const int fr = lane % 32, fk = lane / 32;
+  const int nk = (g.K + BK - 1) / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) gload((kt + 1) * BK);
+    const float* la = lds[kt & 1][0];
+    const float* lb = lds[kt & 1][1];
+#pragma unroll
+    for (int kp = 0; kp < BK / 2; ++kp) {
+      const int row = (2 * kp + fk) * P;
+      float af[2], bfv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = la[row + wm * 64 + i * 32 + fr];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bfv[j] = lb[row + wn * 64 + j * 32 + fr];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bfv[j], af[i], acc[i][j], 0, 0, 0);
+    }
+    if (more) lstore((kt + 1) & 1);
+    __syncthreads();
+  }
+  // lane holds C row m0 + wm*64 + i*32 + lane%32, columns n0 + wn*64 + j*32 + 8*q + 4*(lane/32) .. +4
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int m = m0 + wm * 64 + i * 32 + fr;
+    if (m >= g.M) continue;
+    float* crow = g.c + int64_t(m) * g.scm;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * fk;
+        const f32x4_t v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        if (n + 4 <= g.N && (reinterpret_cast<uintptr_t>(crow + n) & 15) == 0) {
+          *reinterpret_cast<f32x4_t*>(crow + n) = v;
+        } else {
+          for (int e = 0; e < 4 && n + e < g.N; ++e) crow[n + e] = v[e];
+        }
+      }
+  }
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL>
 int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   const int64_t tiles = int64_t((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
@@ -309,11 +494,10 @@ int launch_mfma(const MfmaArgs& g, hipStream_t s) {
 }
 
 // Tile shape by output size (measured on MI355X at the Qwen3-0.6B projections, M = 2048): the largest tile that
-// still gives >= 192 tiles (3/4 of the 256 CUs), small-M tiles for decode batches.
+// still gives >= 192 tiles (3/4 of the 256 CUs); 64x64 tiles for 32 < M <= 64.
 template <int RS, bool KTAIL>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
-  if (g.M <= 32) return launch_mfma<32, 64, 1, 2, RS, KTAIL>(g, s);
   if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL>(g, s);
   if (tiles(256, 256) >= 192) return launch_mfma<256, 256, 4, 2, 1, KTAIL>(g, s);
   if (tiles(128, 256) >= 192) return launch_mfma<128, 256, 2, 2, RS, KTAIL>(g, s);
@@ -321,11 +505,32 @@ int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   return launch_mfma<128, 64, 2, 2, RS, KTAIL>(g, s);
 }
 
+// 8 waves per block; 4 k steps of loads per wave in flight for wide outputs, 8 when N < 2048 (fewer blocks, each
+// with more of W to stream) -- the best of a sweep over 4/8/16 waves and 2/4/8 steps at the Qwen3-0.6B shapes.
+template <int MT>
+int launch_skinny(const MfmaArgs& g, hipStream_t s) {
+  constexpr int NW = 8;
+  const dim3 grid(unsigned((g.N + 15) / 16)), block(NW * 64);
+  if (g.N >= 2048) hipLaunchKernelGGL((gemm_skinny<MT, NW, 4>), grid, block, 0, s, g);
+  else hipLaunchKernelGGL((gemm_skinny<MT, NW, 8>), grid, block, 0, s, g);
+  return check_launch("matmul");
+}
+
 int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
+  if (g.M <= 16) return launch_skinny<1>(g, s);
+  if (g.M <= 32) return launch_skinny<2>(g, s);
   const int nk = (g.K + kBK - 1) / kBK;
   if (g.K % kBK != 0) return launch_mfma_shape<1, true>(g, s);
   if (nk % 2 == 0) return launch_mfma_shape<2, false>(g, s);
   return launch_mfma_shape<1, false>(g, s);
+}
+
+template <bool B_NMAJOR, bool TF32>
+int launch_f32(const F32Args& g, hipStream_t s) {
+  const int64_t tiles = int64_t((g.M + 127) / 128) * ((g.N + 127) / 128);
+  if (tiles > INT32_MAX) return invalid("matmul: matrix too large");
+  hipLaunchKernelGGL((gemm_mfma_f32<B_NMAJOR, TF32>), dim3(unsigned(tiles)), dim3(256), 0, s, g);
+  return check_launch("matmul");
 }
 
 template <typename T, bool TF32>
@@ -365,6 +570,18 @@ extern "C" int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, in
     }
     return launch_generic<uint16_t, false>(g, s);
   }
-  if (precision == NVHIP_PREC_TF32) return launch_generic<float, true>(g, s);
+  // fp32 MFMA path: A K-contiguous, B K- or N-contiguous, 16-byte aligned rows, C with unit column stride
+  const bool tf32 = precision == NVHIP_PREC_TF32;
+  const bool b_kmajor = sbk == 1 && sbn % 4 == 0, b_nmajor = sbn == 1 && sbk % 4 == 0 && N % 4 == 0;
+  const bool mfma = sak == 1 && sam % 4 == 0 && K % 4 == 0 && K > 0 && scn == 1 && (b_kmajor || b_nmajor) &&
+                    aligned16(a) && aligned16(b) &&
+                    M < (int64_t(1) << 31) && N < (int64_t(1) << 31) && K < (int64_t(1) << 31);
+  if (mfma) {
+    F32Args f{static_cast<float*>(c), static_cast<const float*>(a), static_cast<const float*>(b),
+              int(M), int(N), int(K), sam, sbk, sbn, scm};
+    if (b_kmajor) return tf32 ? launch_f32<false, true>(f, s) : launch_f32<false, false>(f, s);
+    return tf32 ? launch_f32<true, true>(f, s) : launch_f32<true, false>(f, s);
+  }
+  if (tf32) return launch_generic<float, true>(g, s);
   return launch_generic<float, false>(g, s);
 }

@@ -29,7 +29,7 @@ TOL = {
 }
 DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16}
 SHAPES = [(1, 1024, 4096), (1, 3072, 1024), (7, 33, 65), (17, 129, 257), (100, 300, 70), (127, 255, 1000),
-          (512, 512, 512), (1000, 1000, 1000), (3, 5, 2)]
+          (512, 512, 512), (1000, 1000, 1000), (3, 5, 2), (130, 260, 36), (20, 100, 200)]
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "matmul_small.npz")
 
 
