@@ -13,7 +13,8 @@ replayed from HIP graphs and timed with HIP events on the stream they run on.
 
 Also reported (under "extra"): the same kernel at T = 1, 32, 2048; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
-and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM.
+and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
+the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s.
 The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
 sample of the same workload.
 
@@ -197,6 +198,7 @@ def extras(torch, oracle, kernels, dev, steps):
                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                          "torch_linear_us": round(ms_ref * 1e3, 2)}
         del a, w0, ws
+    out["paged_decode_attention_B32"] = decode_attention(torch, dev, steps, g)
     n = 4096
     a = torch.randn(n, n, generator=g).to(dev)
     b = torch.randn(n, n, generator=g).to(dev)
@@ -207,6 +209,37 @@ def extras(torch, oracle, kernels, dev, steps):
                                   "frac_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4),
                                   "torch_matmul_us": round(ms_ref * 1e3, 1)}
     return out
+
+
+def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
+    """Paged decode attention of one Qwen3-0.6B layer for a batch of 32 sequences with contexts U[512, 2048]
+    (one query token each), NSETS caches rotated so that the K/V (~170 MB per set) come from HBM.
+    bytes = sum(ctx) * Hkv * D * 2 (k, v) * 2 B + q read + out write + context lengths + block-table entries."""
+    from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
+    lens = torch.randint(min_len, max_len + 1, (batch,), generator=g)
+    need = [(int(n) + BLOCK - 1) // BLOCK for n in lens]
+    nb = sum(need)
+    sets = []
+    for _ in range(NSETS):
+        kc = torch.empty(nb, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev).normal_()
+        vc = torch.empty_like(kc).normal_()
+        perm = torch.randperm(nb, generator=g)
+        bt = torch.zeros(batch, max(need), dtype=torch.int32)
+        used = 0
+        for b, k in enumerate(need):
+            bt[b, :k] = perm[used:used + k].to(torch.int32)
+            used += k
+        q = torch.randn(batch, 1, HQ, D, generator=g).to(torch.bfloat16).to(dev)
+        sets.append((q, kc, vc, lens.to(torch.int32).to(dev), bt.to(dev)))
+    scale = D ** -0.5
+    ms, _ = time_graph(torch, lambda i: flash_attn_with_kvcache(*sets[i % NSETS], scale, True), NSETS,
+                       max(40, steps), 8)
+    ctx = int(lens.sum())
+    nbytes = ctx * HKV * D * 2 * 2 + 2 * batch * HQ * D * 2 + batch * 4 + sum(need) * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del sets
+    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "context_tokens": ctx, "bytes": nbytes}
 
 
 def copy_ceiling(torch, dev, mib=1024, reps=20):

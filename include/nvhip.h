@@ -89,6 +89,25 @@ int nvhip_silu_mul_bf16(void* out, const void* x, int64_t rows, int64_t x_stride
 int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
                  int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype, int precision, void* stream);
 
+/*
+ * Paged decode attention over the KV cache that nvhip_qk_norm_rope_kv_bf16 writes.
+ * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=context_lens, block_table=block_table,
+ * softmax_scale=scale, causal=True) as called at nanovllm/layers/attention.py:84-90 (decode branch).
+ *   q, out: [num_seqs * q_len, Hq, D] bf16; token b*q_len + i, head h at ptr + token*stride_token + h*stride_head,
+ *   elements contiguous (16-byte aligned rows). k_cache, v_cache: [num_blocks, block_size, Hkv, D] bf16 contiguous.
+ *   block_table: [num_seqs, max_blocks] int32 (entries past a sequence's blocks unused; -1 padding allowed).
+ *   context_lens: [num_seqs] int32 cache tokens per sequence, including the q_len new ones (0 = padding: zero
+ *   output). Query i sees cache tokens < context_len - q_len + i + 1 when causal, all context_len otherwise.
+ *   Blocks outside [0, num_blocks) are skipped. D: 64, 128, 256; (Hq / Hkv) * q_len <= 16 (8 for D = 256).
+ * Numerics: fp32 scores and softmax (exp2 with the scale folded in), fp32 P*V accumulation, bf16 output.
+ */
+int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                      const int32_t* block_table, const int32_t* context_lens, int64_t num_seqs,
+                                      int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size,
+                                      int64_t num_blocks, int64_t max_blocks, int64_t q_stride_token,
+                                      int64_t q_stride_head, int64_t out_stride_token, int64_t out_stride_head,
+                                      float scale, int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,8 @@ SIGNATURES = {
     "nvhip_add_rms_norm_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f, _p],
     "nvhip_silu_mul_bf16": [_p, _p, _i64, _i64, _i64, _p],
     "nvhip_matmul": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _p],
+    "nvhip_paged_decode_attention_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                          _i64, _i64, _i64, _i64, _f, _i, _p],
 }
 
 _lib = None

@@ -11,8 +11,12 @@ eager), for each request that diverges the first divergent step and the torch ba
 candidates there (a near-tie flipped by a last-bit difference has a tiny gap), the graph replay time per decode step
 and the number of kernel nodes in each decode graph.
 
+The attention of the decode steps (shared by both backends) is the HIP paged decode attention by default
+(--attention torch: the harness's fp32 torch code).
+
 Usage: python -m nanovllm_hip.harness.decode [--batch 32] [--steps 32] [--layers 28] [--min-len 512]
                                              [--max-len 2048] [--seed 0] [--reps 20] [--fp32-logits]
+                                             [--attention hip|torch]
 """
 import argparse
 import ctypes
@@ -68,8 +72,9 @@ def prefill(model, batch, backend, fp32_logits=False, reference=None):
 class DecodeStep:
     """Static input buffers of one decode step and the step itself (eager or replayed from a graph)."""
 
-    def __init__(self, model, batch, backend, fp32_logits=False):
+    def __init__(self, model, batch, backend, fp32_logits=False, attention="hip"):
         self.model, self.batch, self.backend, self.fp32_logits = model, batch, backend, fp32_logits
+        self.attention = attention
         B, dev = len(batch.lens), batch.device
         self.input_ids = torch.zeros(B, dtype=torch.int64, device=dev)
         self.positions = torch.zeros(B, dtype=torch.int64, device=dev)
@@ -89,7 +94,7 @@ class DecodeStep:
 
     def forward(self):
         ctx = Context(False, self.slot_mapping, self.context_lens, self.batch.block_tables)
-        h = self.model.forward(self.input_ids, self.positions, ctx, self.backend)
+        h = self.model.forward(self.input_ids, self.positions, ctx, self.backend, self.attention)
         logits = self.model.logits(h, self.fp32_logits)
         return logits, logits.argmax(dim=-1)
 
@@ -113,9 +118,9 @@ class DecodeStep:
 
 
 @torch.inference_mode()
-def decode(model, batch, first, steps, backend, use_graph, reference=None, fp32_logits=False):
+def decode(model, batch, first, steps, backend, use_graph, reference=None, fp32_logits=False, attention="hip"):
     """Greedy decode of `steps` tokens after `first`; returns (tokens [B][steps], divergence info vs reference)."""
-    step = DecodeStep(model, batch, backend, fp32_logits)
+    step = DecodeStep(model, batch, backend, fp32_logits, attention)
     if use_graph:
         step.set_inputs(first, 0)
         step.capture()
@@ -181,8 +186,10 @@ def main(argv=None):
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--reps", type=int, default=20)
     p.add_argument("--fp32-logits", action="store_true", help="LM head in fp32 (both backends)")
+    p.add_argument("--attention", choices=("hip", "torch"), default="hip",
+                   help="decode attention of both backends: HIP paged kernel or the fp32 torch code")
     args = p.parse_args(argv)
-    f32 = args.fp32_logits
+    f32, att = args.fp32_logits, args.attention
     dev = torch.device("cuda:0")
     cfg = Qwen3Config(num_hidden_layers=args.layers)
     t0 = time.time()
@@ -190,16 +197,18 @@ def main(argv=None):
     batch = Batch(cfg, args.batch, args.steps, args.min_len, args.max_len, args.seed, dev)
     out = {"config": {"model": "Qwen3-0.6B shapes, random init", "layers": args.layers, "batch": args.batch,
                       "steps": args.steps, "prompt_lens": [args.min_len, args.max_len], "kv_blocks": batch.num_blocks,
-                      "block_size": BLOCK, "lm_head": "fp32" if f32 else "bf16"}}
+                      "block_size": BLOCK, "lm_head": "fp32" if f32 else "bf16",
+                      "decode_attention": att}}
     print(f"model + batch ready in {time.time() - t0:.1f}s; prompts {sum(batch.lens)} tokens", flush=True)
 
     # hip backend: prefill, eager decode, graph decode from the same KV state
     cache = model.allocate_kv_cache(batch.num_blocks)
     first_h, _ = prefill(model, batch, "hip", f32)
     snapshot = cache.clone()
-    tok_h, _, _ = decode(model, batch, first_h, args.steps, "hip", use_graph=False, fp32_logits=f32)
+    tok_h, _, _ = decode(model, batch, first_h, args.steps, "hip", use_graph=False, fp32_logits=f32, attention=att)
     cache.copy_(snapshot)
-    tok_hg, _, step_hg = decode(model, batch, first_h, args.steps, "hip", use_graph=True, fp32_logits=f32)
+    tok_hg, _, step_hg = decode(model, batch, first_h, args.steps, "hip", use_graph=True, fp32_logits=f32,
+                                attention=att)
     print("hip backend done", flush=True)
     # torch backend (the reference): eager decode, compared step by step with the hip tokens (while a request's
     # history is identical its logits are directly comparable), then graph decode
@@ -207,9 +216,10 @@ def main(argv=None):
     first_t, div_prefill = prefill(model, batch, "torch", f32, reference=first_h)
     snapshot.copy_(cache)
     tok_t, div, _ = decode(model, batch, first_t, args.steps, "torch", use_graph=False, reference=tok_h,
-                        fp32_logits=f32)
+                        fp32_logits=f32, attention=att)
     cache.copy_(snapshot)
-    tok_tg, _, step_tg = decode(model, batch, first_t, args.steps, "torch", use_graph=True, fp32_logits=f32)
+    tok_tg, _, step_tg = decode(model, batch, first_t, args.steps, "torch", use_graph=True, fp32_logits=f32,
+                                attention=att)
     print("torch backend done", flush=True)
     div = {b: d for b, d in div.items() if first_h[b] == first_t[b]}
     div.update(div_prefill)

@@ -8,8 +8,11 @@ backend "hip"   : rms_norm / fused_add_rms_norm_ (residual in place) / silu_and_
                   nanovllm_hip.kernels (the fused kernel does q/k norm, RoPE and the KV write in one launch).
 backend "torch" : the layers' own torch code run eagerly (what the reference's "compile" backend compiles), with
                   the unfused q_norm, k_norm, rotary and KV scatter.
-Both backends share everything else: the projections (torch F.linear), the embedding / tied LM head, and the paged
-attention below, so that token differences between them come only from the four kernels.
+Both backends share everything else: the projections (torch F.linear), the embedding / tied LM head, and the
+attention, so that token differences between them come only from the four kernels. The attention is chosen apart
+from the backend: "torch" = the fp32 code below (prefill and decode), "hip" = the HIP paged decode attention
+(nanovllm_hip.kernels.attention, the flash_attn_with_kvcache call of layers/attention.py:84-90) for decode steps,
+the fp32 code for prefill.
 """
 from dataclasses import dataclass
 
@@ -17,6 +20,7 @@ import torch
 import torch.nn.functional as F
 
 from nanovllm_hip import kernels as hip
+from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
 
 
 @dataclass
@@ -161,7 +165,7 @@ class Qwen3:
         self.kv = [(cache[0, i], cache[1, i]) for i in range(c.num_hidden_layers)]
         return cache
 
-    def forward(self, input_ids, positions, ctx: Context, backend: str):
+    def forward(self, input_ids, positions, ctx: Context, backend: str, attention: str = "torch"):
         """Returns the final hidden states [T, hidden] (after the last norm)."""
         c = self.cfg
         eps = c.rms_norm_eps
@@ -195,6 +199,10 @@ class Qwen3:
                 store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
             if ctx.is_prefill:
                 o = prefill_attention(q, k, v, self.scale)
+            elif attention == "hip":
+                B = ctx.context_lens.shape[0]
+                o = flash_attn_with_kvcache(q.view(B, -1, hq, D), k_cache, v_cache, ctx.context_lens,
+                                            ctx.block_tables, self.scale, causal=True).view(-1, hq, D)
             else:
                 o = paged_decode_attention(q, k_cache, v_cache, ctx.block_tables, ctx.context_lens, self.scale)
             h = F.linear(o.reshape(o.shape[0], hq * D), L["o"])

@@ -22,6 +22,8 @@ _DEF.define("fused_add_rms_norm(Tensor x, Tensor residual, Tensor w, float eps) 
 _DEF.define("fused_add_rms_norm_(Tensor x, Tensor(a!) residual, Tensor w, float eps) -> Tensor")
 _DEF.define("silu_and_mul(Tensor x) -> Tensor")
 _DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
+_DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
+            "Tensor context_lens, int q_len, float scale, bool causal) -> Tensor")
 
 
 # ------------------------------------------------------------------ qk_norm_rope_kv
@@ -156,3 +158,26 @@ _DEF.impl("matmul", _matmul_impl, "CUDA")
 @torch.library.register_fake("nvhip::matmul")
 def _matmul_fake(a, b, input_precision):
     return torch.empty((a.shape[0], b.shape[1]), dtype=a.dtype, device=a.device)
+
+
+# ------------------------------------------------------------------ paged decode attention
+
+def _paged_decode_attention_impl(q, k_cache, v_cache, block_table, context_lens, q_len, scale, causal):
+    T, Hq, D = q.shape
+    num_blocks, block_size, Hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
+    status = _lib.lib().nvhip_paged_decode_attention_bf16(
+        out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+        context_lens.data_ptr(), context_lens.shape[0], q_len, Hq, Hkv, D, block_size, num_blocks,
+        block_table.shape[1], q.stride(0), q.stride(1), out.stride(0), out.stride(1), scale, int(causal),
+        _lib.stream_of(q))
+    _lib.check(status, "paged_decode_attention")
+    return out
+
+
+_DEF.impl("paged_decode_attention", _paged_decode_attention_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::paged_decode_attention")
+def _paged_decode_attention_fake(q, k_cache, v_cache, block_table, context_lens, q_len, scale, causal):
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)

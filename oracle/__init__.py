@@ -15,6 +15,10 @@ Functions and the reference code each one follows (paths in R3pere/nano-vllm-tri
                      that nanovllm/kernels/qk_norm_rope_kv.py:92-125 replaces)
   silu_and_mul       nanovllm/layers/activation.py:15-18
   matmul_fp64        tests/test_kernels_matmul.py:52 (A.double() @ B.double())
+  paged_decode_attention  nanovllm/layers/attention.py:84-90 (flash_attn_with_kvcache on the paged cache, decode),
+                     slot formula model_runner.py:340; flash-attn is not vendored in the reference (an unpinned
+                     pyproject dependency), so its documented semantics (bottom-right causal mask, GQA head h -> kv
+                     head h // (Hq / Hkv)) are restated and pinned by float64 SDPA, closed forms and invariants
 
 How each is pinned (tests/test_oracle.py): closed forms in float64, hand-computed known answers, invariants
 (identity rotation, norm preservation, relative-position dependence, scale invariance), and brute-force loops on
@@ -24,6 +28,7 @@ from oracle.torch_ref import (  # noqa: F401
     add_rms_forward,
     apply_rotary_emb,
     matmul_fp64,
+    paged_decode_attention,
     qk_norm_rope_kv,
     rms_forward,
     rope_cos_sin_cache,

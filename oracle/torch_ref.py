@@ -92,3 +92,40 @@ def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
 def matmul_fp64(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """The GEMM reference of tests/test_kernels_matmul.py:52: exact-ish float64 product of the inputs."""
     return a.double() @ b.double()
+
+
+def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, context_lens: torch.Tensor,
+                           block_table: torch.Tensor, scale: float, causal: bool = True,
+                           compute_dtype=torch.float32) -> torch.Tensor:
+    """The decode call of layers/attention.py:84-90, flash_attn_with_kvcache(q, k_cache, v_cache,
+    cache_seqlens=context_lens, block_table=block_table, softmax_scale=scale, causal=True), restated.
+
+    q [num_seqs, q_len, Hq, D]; caches [num_blocks, block_size, Hkv, D] (model_runner.py:262-267); block_table
+    [num_seqs, max_blocks] int32; context_lens [num_seqs] int32. Cache token j of sequence b is slot
+    block_table[b, j // block_size] * block_size + j % block_size (model_runner.py:340). Query i of a sequence with
+    L cached tokens sees tokens j <= L - q_len + i when causal (the mask is aligned to the bottom right, as the comment
+    at attention.py:86 says), all L otherwise; head h reads kv head h // (Hq / Hkv). softmax(q.k * scale) @ v in
+    compute_dtype, output in q's dtype; a query that sees no token gets zeros."""
+    num_seqs, q_len, Hq, D = q.shape
+    block_size, Hkv = k_cache.shape[1], k_cache.shape[2]
+    g = Hq // Hkv
+    out = torch.zeros(q.shape, dtype=compute_dtype)
+    kf = k_cache.reshape(-1, Hkv, D)
+    vf = v_cache.reshape(-1, Hkv, D)
+    for b in range(num_seqs):
+        L = int(context_lens[b])
+        if L <= 0:
+            continue
+        j = torch.arange(L)
+        slots = block_table[b].long()[j // block_size] * block_size + j % block_size
+        kb = kf[slots].to(compute_dtype).repeat_interleave(g, dim=1)   # [L, Hq, D]
+        vb = vf[slots].to(compute_dtype).repeat_interleave(g, dim=1)
+        qb = q[b].to(compute_dtype)                                    # [q_len, Hq, D]
+        s = torch.einsum("ihd,jhd->hij", qb, kb) * scale               # [Hq, q_len, L]
+        if causal:
+            limit = L - q_len + torch.arange(q_len)                    # last visible token of query i
+            s = s.masked_fill(j[None, None, :] > limit[None, :, None], float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        p = torch.nan_to_num(p, nan=0.0)                               # queries that see nothing
+        out[b] = torch.einsum("hij,jhd->ihd", p, vb)
+    return out.to(q.dtype)

@@ -1,6 +1,7 @@
 """End-to-end greedy decode through the HIP kernels (GPU): a random-init Qwen3-0.6B-shaped model (2 layers here, to
 keep the test short; bench runs of the harness use all 28), batch 4, prompts of 100-300 random tokens, paged KV in
-256-slot blocks, 8 decode steps, eager and HIP-graph decode.
+256-slot blocks, 8 decode steps, eager and HIP-graph decode, with the HIP paged decode attention (and once with the
+fp32 torch attention) shared by both backends.
 
 Checks: the graph replay gives exactly the eager tokens (both backends); the hip backend's tokens equal the
 torch-eager backend's, except where the torch backend's own logits had the two candidates within one bf16 step of
@@ -15,9 +16,10 @@ from nanovllm_hip.harness import decode
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("fp32_logits", [False, True])
-def test_decode_hip_vs_torch(fp32_logits):
-    args = ["--layers", "2", "--batch", "4", "--steps", "8", "--min-len", "100", "--max-len", "300", "--reps", "2"]
+@pytest.mark.parametrize("attention,fp32_logits", [("hip", False), ("hip", True), ("torch", False)])
+def test_decode_hip_vs_torch(attention, fp32_logits):
+    args = ["--layers", "2", "--batch", "4", "--steps", "8", "--min-len", "100", "--max-len", "300", "--reps", "2",
+            "--attention", attention]
     out = decode.main(args + (["--fp32-logits"] if fp32_logits else []))
     assert out["graph_equals_eager"] == {"hip": True, "torch": True}
     agree = out["tokens_hip_vs_torch_eager"]

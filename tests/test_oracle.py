@@ -14,6 +14,10 @@ divisor, a missing rounding, a transposed operand) fails at least one check:
   qk_norm_rope_kv   identity rotation reduces it to the norms; cache rows equal k_out / raw v; empty cache no-op
   silu_and_mul      float64 closed form; known answers at 0 and large |g|; gate/up order
   matmul_fp64       brute-force triple loop on the reference's tiny shapes
+  paged_decode_attention  float64 torch SDPA on the gathered, GQA-expanded K/V with an explicit bottom-right mask;
+                    equal keys give the mean of exactly the visible values (visible count, head mapping); a dominant
+                    key one past the causal limit does not leak in, one at the limit wins; relocating blocks, -1
+                    padding and NaN in unused slots change nothing; an empty context gives zeros
 """
 import math
 
@@ -282,3 +286,101 @@ def test_matmul_fp64_brute_force(M, N, K):
         for j in range(N):
             assert abs(c[i, j] - math.fsum(al[i][kk] * bl[kk][j] for kk in range(K))) < 1e-9
     assert c.shape == (M, N)
+
+
+# ------------------------------------------------------------------ paged decode attention
+
+def _paged_setup(num_seqs=3, q_len=1, Hq=4, Hkv=2, D=16, block_size=8, lens=(5, 17, 9), seed=0, num_blocks=12):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(num_seqs, q_len, Hq, D, generator=g, dtype=torch.float64)
+    kc = torch.randn(num_blocks, block_size, Hkv, D, generator=g, dtype=torch.float64)
+    vc = torch.randn(num_blocks, block_size, Hkv, D, generator=g, dtype=torch.float64)
+    perm = torch.randperm(num_blocks, generator=g)
+    maxb = max((n + block_size - 1) // block_size for n in lens)
+    bt = torch.full((num_seqs, maxb), -1, dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(lens):
+        nb = (n + block_size - 1) // block_size
+        bt[b, :nb] = perm[used:used + nb].to(torch.int32)
+        used += nb
+    return q, kc, vc, torch.tensor(lens, dtype=torch.int32), bt
+
+
+def _gather(cache, bt_row, n, block_size):
+    j = torch.arange(n)
+    return cache.reshape(-1, *cache.shape[2:])[bt_row.long()[j // block_size] * block_size + j % block_size]
+
+
+@pytest.mark.parametrize("q_len,causal", [(1, True), (3, True), (3, False)])
+def test_paged_attention_matches_sdpa_float64(q_len, causal):
+    """Against torch's scaled_dot_product_attention in float64 on the gathered, GQA-expanded K/V with an explicit
+    bottom-right causal mask."""
+    q, kc, vc, lens, bt = _paged_setup(q_len=q_len)
+    scale = 0.3
+    out = oracle.paged_decode_attention(q, kc, vc, lens, bt, scale, causal, compute_dtype=torch.float64)
+    for b in range(q.shape[0]):
+        n = int(lens[b])
+        k = _gather(kc, bt[b], n, 8).repeat_interleave(2, dim=1).permute(1, 0, 2)   # [Hq, n, D]
+        v = _gather(vc, bt[b], n, 8).repeat_interleave(2, dim=1).permute(1, 0, 2)
+        mask = torch.ones(q_len, n, dtype=torch.bool)
+        if causal:
+            mask = torch.arange(n)[None, :] <= (n - q_len + torch.arange(q_len))[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(q[b].permute(1, 0, 2), k, v, attn_mask=mask,
+                                                               scale=scale)
+        torch.testing.assert_close(out[b], ref.permute(1, 0, 2), rtol=1e-12, atol=1e-12)
+
+
+def test_paged_attention_uniform_keys_average_visible_values():
+    """Equal keys: every visible token gets the same weight, so query i of a causal step with L tokens returns the
+    mean of the first L - q_len + i + 1 values -- pins the visible count of each query and the GQA head mapping."""
+    q, kc, vc, lens, bt = _paged_setup(q_len=3)
+    kc[:] = 0.7
+    out = oracle.paged_decode_attention(q, kc, vc, lens, bt, 0.5, True, compute_dtype=torch.float64)
+    for b in range(3):
+        n = int(lens[b])
+        v = _gather(vc, bt[b], n, 8)                                               # [n, Hkv, D]
+        for i in range(3):
+            visible = n - 3 + i + 1
+            for h in range(4):
+                expect = v[:visible, h // 2].mean(dim=0)
+                torch.testing.assert_close(out[b, i, h], expect, rtol=1e-12, atol=1e-12)
+
+
+def test_paged_attention_causal_boundary_and_layout_invariance():
+    """A dominant key right after a query's last visible token must not leak in, one at the last visible token
+    must win; moving blocks (and the table with them), -1 padding and NaN in unused slots change nothing."""
+    q, kc, vc, lens, bt = _paged_setup(q_len=2, lens=(20, 20, 20), num_blocks=10)
+    bs = 8
+    base = oracle.paged_decode_attention(q, kc, vc, lens, bt, 1.0, True, compute_dtype=torch.float64)
+    # query 0 sees tokens <= 18; plant at token 19 a key aligned with query 1's head 0 (score ~ 50 |q|, far above
+    # the others) -> query 0 unchanged, query 1 head 0 returns that token's value
+    big_k = kc.clone()
+    slot = int(bt[0, 19 // bs]) * bs + 19 % bs
+    big_k.view(-1, 2, 16)[slot, 0] = 50 * q[0, 1, 0] / q[0, 1, 0].norm()
+    out = oracle.paged_decode_attention(q, big_k, vc, lens, bt, 1.0, True, compute_dtype=torch.float64)
+    torch.testing.assert_close(out[0, 0], base[0, 0])
+    torch.testing.assert_close(out[0, 1, 0], vc.view(-1, 2, 16)[slot, 0], rtol=1e-9, atol=1e-9)
+    # relocate every block to a new physical block, fill the unused slots and the old blocks with NaN
+    perm = torch.randperm(10, generator=torch.Generator().manual_seed(5))
+    kc2 = torch.full((20, bs, 2, 16), float("nan"), dtype=torch.float64)
+    vc2 = kc2.clone()
+    bt2 = bt.clone()
+    for b in range(3):
+        for c in range(bt.shape[1]):
+            if bt[b, c] >= 0:
+                dst = int(perm[bt[b, c]]) + 10
+                kc2[dst], vc2[dst] = kc[bt[b, c]], vc[bt[b, c]]
+                bt2[b, c] = dst
+    for b in range(3):   # slots past the context inside the last block hold NaN
+        last = (20 - 1) // bs
+        kc2[bt2[b, last], 20 % bs:] = float("nan")
+        vc2[bt2[b, last], 20 % bs:] = float("nan")
+    out2 = oracle.paged_decode_attention(q, kc2, vc2, lens, bt2, 1.0, True, compute_dtype=torch.float64)
+    torch.testing.assert_close(out2, base, rtol=0, atol=0)
+
+
+def test_paged_attention_empty_context_is_zero():
+    q, kc, vc, lens, bt = _paged_setup()
+    lens[1] = 0
+    out = oracle.paged_decode_attention(q, kc, vc, lens, bt, 1.0, True, compute_dtype=torch.float64)
+    assert torch.all(out[1] == 0)

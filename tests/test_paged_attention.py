@@ -1,0 +1,135 @@
+"""GPU parity of the paged decode attention (nvhip_paged_decode_attention_bf16) against the oracle.
+
+The oracle restates flash_attn_with_kvcache as nanovllm/layers/attention.py:84-90 calls it (fp32 from the same
+bf16 inputs). Tolerance: the bf16 output tolerance rtol 1.6e-2, atol 1e-2. Cases: the Qwen3-0.6B decode batch
+(32 sequences, 16 q heads, 8 kv heads, head_dim 128, 256-slot blocks, contexts of 512..2048 tokens); context lengths
+around the 32-token chunk and the block size, 0 (padding) and 1; block sizes that are not a multiple of 32; head_dim
+64 and 256; GQA ratios 1, 4, 8; several query tokens per sequence with and without the causal mask; NaN in the
+unused slots of a sequence's last block and in blocks no sequence owns; graph capture and replay.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make_case(lens, q_len=1, Hq=16, Hkv=8, D=128, block_size=256, seed=0, spare_blocks=3, nan_unused=True):
+    g = torch.Generator("cpu").manual_seed(seed)
+    num_seqs = len(lens)
+    need = [max(1, (n + block_size - 1) // block_size) for n in lens]
+    num_blocks = sum(need) + spare_blocks
+    kc = torch.randn(num_blocks, block_size, Hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(num_blocks, block_size, Hkv, D, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(num_blocks, generator=g)
+    maxb = max(need)
+    bt = torch.full((num_seqs, maxb), -1, dtype=torch.int32)
+    used = 0
+    for b, nb in enumerate(need):
+        bt[b, :nb] = perm[used:used + nb].to(torch.int32)
+        used += nb
+    if nan_unused:
+        for b, n in enumerate(lens):   # slots past the context in the sequence's last block
+            last = int(bt[b, max(n - 1, 0) // block_size])
+            if n % block_size:
+                kc[last, n % block_size:] = float("nan")
+                vc[last, n % block_size:] = float("nan")
+        for blk in perm[used:]:          # blocks no sequence owns
+            kc[blk] = float("nan")
+            vc[blk] = float("nan")
+    q = torch.randn(num_seqs, q_len, Hq, D, generator=g).to(torch.bfloat16)
+    return q, kc, vc, torch.tensor(lens, dtype=torch.int32), bt
+
+
+def run_and_check(q, kc, vc, lens, bt, causal=True, scale=None):
+    D = q.shape[-1]
+    scale = D ** -0.5 if scale is None else scale
+    out = flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV), lens.to(DEV), bt.to(DEV), scale, causal)
+    ref = oracle.paged_decode_attention(q, kc, vc, lens, bt, scale, causal)
+    out = out.cpu()
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    assert torch.isfinite(out.float()).all()
+    torch.testing.assert_close(out.float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+    return out, ref
+
+
+def test_qwen3_decode_batch():
+    g = torch.Generator("cpu").manual_seed(7)
+    lens = torch.randint(512, 2049, (32,), generator=g).tolist()
+    out, ref = run_and_check(*make_case(lens))
+    # fp32 inside, one bf16 rounding at the end: nearly every element is the correctly rounded oracle value
+    assert (out == ref).float().mean() > 0.97
+
+
+@pytest.mark.parametrize("block_size", [256, 32, 16, 8])
+def test_context_lengths_around_chunks_and_blocks(block_size):
+    lens = [1, 2, 31, 32, 33, 63, 64, 65, 255, 256, 257, 300, 511, 513]
+    run_and_check(*make_case(lens, block_size=block_size, seed=block_size))
+
+
+def test_padding_sequence_gets_zeros():
+    q, kc, vc, lens, bt = make_case([40, 0, 70], nan_unused=False)
+    out, _ = run_and_check(q, kc, vc, lens, bt)
+    assert torch.all(out[1] == 0)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_head_dims(D):
+    run_and_check(*make_case([5, 100, 700], D=D, Hq=8, Hkv=4, seed=D))
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 4), (16, 2)])
+def test_gqa_ratios(Hq, Hkv):
+    run_and_check(*make_case([77, 300, 1000], Hq=Hq, Hkv=Hkv, seed=Hq * 10 + Hkv))
+
+
+@pytest.mark.parametrize("q_len,causal", [(2, True), (3, True), (4, False), (8, True)])
+def test_several_query_tokens(q_len, causal):
+    run_and_check(*make_case([q_len, 50, 290, 1024], q_len=q_len, Hq=16, Hkv=8, seed=q_len), causal=causal)
+
+
+def test_sixteen_rows_per_kv_head():
+    run_and_check(*make_case([20, 600], q_len=2, Hq=8, Hkv=1, seed=3))
+
+
+def test_strided_q_view():
+    """q as a view of a wider buffer (per-token stride > Hq * D) is accepted (copied by the wrapper)."""
+    q, kc, vc, lens, bt = make_case([100, 200])
+    wide = torch.zeros(2, 1, 16, 160, dtype=torch.bfloat16)
+    wide[..., :128] = q
+    run_and_check(wide[..., :128], kc, vc, lens, bt)
+
+
+def test_graph_replay_matches_eager():
+    q, kc, vc, lens, bt = make_case([300, 700, 1500, 64], seed=11)
+    q, kc, vc, lens, bt = (t.to(DEV) for t in (q, kc, vc, lens, bt))
+    eager = flash_attn_with_kvcache(q, kc, vc, lens, bt, 128 ** -0.5, True)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        flash_attn_with_kvcache(q, kc, vc, lens, bt, 128 ** -0.5, True)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(graph):
+        out = flash_attn_with_kvcache(q, kc, vc, lens, bt, 128 ** -0.5, True)
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+
+
+def test_rejects_bad_arguments():
+    q, kc, vc, lens, bt = (t.to(DEV) for t in make_case([10, 20]))
+    with pytest.raises(AssertionError):
+        flash_attn_with_kvcache(q.float(), kc, vc, lens, bt, 0.1, True)
+    with pytest.raises(ValueError):   # 32 rows per kv head
+        flash_attn_with_kvcache(q.repeat(1, 2, 1, 1), kc[:, :, :1].contiguous(), vc[:, :, :1].contiguous(), lens, bt,
+                                0.1, True)
