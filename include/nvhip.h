@@ -99,6 +99,9 @@ int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, int64_t N, in
  *   context_lens: [num_seqs] int32 cache tokens per sequence, including the q_len new ones (0 = padding: zero
  *   output). Query i sees cache tokens < context_len - q_len + i + 1 when causal, all context_len otherwise.
  *   Blocks outside [0, num_blocks) are skipped. D: 64, 128, 256; (Hq / Hkv) * q_len <= 16 (8 for D = 256).
+ *   workspace: device memory of at least nvhip_paged_decode_attention_workspace_size(...) bytes (contents need no
+ *   initialisation; used by this call only) lets long contexts be split over several blocks and merged by a second
+ *   kernel; NULL (or too small) runs one block per (sequence, kv head).
  * Numerics: fp32 scores and softmax (exp2 with the scale folded in), fp32 P*V accumulation, bf16 output.
  */
 int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_cache, const void* v_cache,
@@ -106,7 +109,15 @@ int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_ca
                                       int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size,
                                       int64_t num_blocks, int64_t max_blocks, int64_t q_stride_token,
                                       int64_t q_stride_head, int64_t out_stride_token, int64_t out_stride_head,
-                                      float scale, int causal, void* stream);
+                                      float scale, int causal, void* workspace, int64_t workspace_size,
+                                      void* stream);
+
+/*
+ * Bytes of workspace nvhip_paged_decode_attention_bf16 uses for these sizes (0: it does not split). Host-only, no
+ * GPU work. An addition of this library (the reference has no workspace: flash-attn allocates its own).
+ */
+int64_t nvhip_paged_decode_attention_workspace_size(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv,
+                                                    int64_t D, int64_t block_size, int64_t max_blocks);
 
 #ifdef __cplusplus
 }

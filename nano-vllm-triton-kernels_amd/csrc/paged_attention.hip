@@ -21,8 +21,15 @@
 //   4. accumulates O[row][dims] = O * rescale + sum p * V in fp32 with the lane-owns-8-dims layout of step 1.
 // At the end the 4 token groups of a wave are summed with lane shuffles and the 8 waves' (max, sum, O) are merged
 // through LDS in wave order (deterministic), O / sum rounded to bf16.
+// The block-table entries of the block's token range are loaded once, one per lane, alongside the context length
+// and Q.
+// Small batches: with a caller workspace the context of each (sequence, kv head) is split over several blocks
+// (whole 256-token rounds) when there are fewer pairs than CUs; each block writes its merged (max, sum, O) record
+// and a second kernel merges the records in split order. Without a workspace one block covers the whole context.
 // Tokens past the context, blocks outside [0, num_blocks) and rows past a query's causal limit take no part (their
 // K/V are not read; p = 0).
+#include <algorithm>
+
 #include "common.h"
 
 namespace nvhip {
@@ -45,6 +52,9 @@ struct DecodeArgs {
   int64_t q_st, q_sh, o_st, o_sh;
   float scale_log2;  // softmax scale * log2(e)
   int causal;
+  int splits;     // context splits per (sequence, kv head): blocks s = 0 .. splits-1 take tokens
+  int split_len;  // [s * split_len, (s + 1) * split_len); a multiple of kChunk * kWaves
+  float* ws;      // splits > 1: [num_seqs, Hkv, splits, RP, 2 + D] fp32 records (max, sum, O) of each block
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -76,26 +86,32 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
   __shared__ float red_acc[kWaves][RP][D];
   __shared__ float red_m[kWaves][RP], red_l[kWaves][RP];
 
-  const int b = blockIdx.x / g.Hkv, kvh = blockIdx.x % g.Hkv;
-  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
+  const int b = pair / g.Hkv, kvh = pair % g.Hkv;
+  const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   const int rows = g.G * g.q_len;
-  const int ctx = min(max(g.ctx_lens[b], 0), g.max_blocks * g.bs);
   const int32_t* bt_row = g.bt + int64_t(b) * g.max_blocks;
+  const int tok_begin = split * g.split_len, blk0 = tok_begin / g.bs;
+  // issued together: the context length, this split's first 64 block-table entries (one per lane), the Q rows
+  const int ctx = min(max(g.ctx_lens[b], 0), g.max_blocks * g.bs);
+  const int bt_lane = blk0 + lane < g.max_blocks ? bt_row[blk0 + lane] : -1;
 
   // Q rows as the MFMA B operand: lane l holds row l % 16, dims 32c + 8 (l / 16) .. +8
   const int qrow = lane % 16, q8 = (lane / 16) * 8;
   bf16x8_t qf[KC];
-  int row_limit = 0;  // row qrow sees tokens < row_limit
+  int qi = 0;  // query token of row qrow
   if (qrow < rows) {
-    const int i = qrow / g.G, hh = qrow % g.G;
-    const uint16_t* qp = g.q + int64_t(b * g.q_len + i) * g.q_st + int64_t(kvh * g.G + hh) * g.q_sh + q8;
+    qi = qrow / g.G;
+    const int hh = qrow % g.G;
+    const uint16_t* qp = g.q + int64_t(b * g.q_len + qi) * g.q_st + int64_t(kvh * g.G + hh) * g.q_sh + q8;
 #pragma unroll
     for (int c = 0; c < KC; ++c) qf[c] = load_bf16x8(qp + 32 * c);
-    row_limit = g.causal ? min(max(ctx - g.q_len + i + 1, 0), ctx) : ctx;
   } else {
 #pragma unroll
     for (int c = 0; c < KC; ++c) qf[c] = bf16x8_t{};
   }
+  // row qrow sees tokens < row_limit
+  const int row_limit = qrow >= rows ? 0 : g.causal ? min(max(ctx - g.q_len + qi + 1, 0), ctx) : ctx;
 
   float m_run = -INFINITY;  // running max of row qrow (the same in the 4 lanes of the row)
   float l_run = 0.0f;       // this lane's part of the row sum
@@ -105,44 +121,61 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
   const int dg = lane % LPT, ts = lane / LPT;
-  const int nchunks = (ctx + kChunk - 1) / kChunk;
+  const int tok_end = min(ctx, tok_begin + g.split_len);
+  const int ch_end = (tok_end + kChunk - 1) / kChunk;
 
-  for (int ch = wave; ch < nchunks; ch += kWaves) {
+  // A chunk's K and V fragments (registers) and which of its tokens are valid. Every load instruction is issued
+  // by all lanes (a lane whose token is not valid reads the first 16 bytes of q) and the loaded values are used as
+  // they are -- invalid tokens are masked out of the scores, so their p is 0 -- so no select waits on a load.
+  struct Tile {
+    bf16x8_t k[2][KC];
+    bf16x8_t v[PVI];
+    uint64_t kvalid[2];  // bit j: token t0 + 16u + j has a valid block (from lanes j = 0..15)
+  };
+  auto row_of = [&](int t, int64_t base, int t0) -> int64_t {
+    if (t >= ctx) return -1;
+    if constexpr (ALIGNED) return base < 0 ? -1 : base + int64_t(t - t0) * g.Hkv * D;
+    return token_row<D>(g, bt_row, t, kvh);
+  };
+  auto load_tile = [&](Tile& T, int ch) {
     const int t0 = ch * kChunk;
     int64_t base = -1;  // ALIGNED: row offset of token t0; tokens t0 + j follow at + j * Hkv * D
-    if constexpr (ALIGNED) base = token_row<D>(g, bt_row, t0, kvh);
-    auto row_of = [&](int t) -> int64_t {
-      if (t >= ctx) return -1;
-      if constexpr (ALIGNED) return base < 0 ? -1 : base + int64_t(t - t0) * g.Hkv * D;
-      return token_row<D>(g, bt_row, t, kvh);
-    };
-    bf16x8_t kf[2][KC], vf[PVI];
+    if constexpr (ALIGNED) {
+      const int idx = t0 / g.bs - blk0;
+      const int blk = idx < 64 ? __builtin_amdgcn_readlane(bt_lane, idx) : bt_row[t0 / g.bs];
+      base = (blk < 0 || blk >= g.num_blocks) ? -1 : ((int64_t(blk) * g.bs + t0 % g.bs) * g.Hkv + kvh) * D;
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int64_t row = row_of(t0 + 16 * u + lane % 16);
+      const int64_t row = row_of(t0 + 16 * u + lane % 16, base, t0);
+      T.kvalid[u] = __ballot(row >= 0);
 #pragma unroll
-      for (int c = 0; c < KC; ++c) kf[u][c] = row >= 0 ? load_bf16x8(g.kc + row + 32 * c + q8) : bf16x8_t{};
+      for (int c = 0; c < KC; ++c) T.k[u][c] = load_bf16x8(row >= 0 ? g.kc + row + 32 * c + q8 : g.q);
     }
 #pragma unroll
     for (int it = 0; it < PVI; ++it) {
-      const int64_t row = row_of(t0 + it * TPI + ts);
-      vf[it] = row >= 0 ? load_bf16x8(g.vc + row + 8 * dg) : bf16x8_t{};
+      const int64_t row = row_of(t0 + it * TPI + ts, base, t0);
+      T.v[it] = load_bf16x8(row >= 0 ? g.vc + row + 8 * dg : g.q);
     }
+  };
+  auto compute_tile = [&](const Tile& T, int ch) {
+    const int t0 = ch * kChunk;
     // scores: lane holds tokens t0 + 16u + 4 (l / 16) + r of row qrow
     f32x4_t s[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       s[u] = f32x4_t{0, 0, 0, 0};
 #pragma unroll
-      for (int c = 0; c < KC; ++c) s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u][c], qf[c], s[u], 0, 0, 0);
+      for (int c = 0; c < KC; ++c) s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(T.k[u][c], qf[c], s[u], 0, 0, 0);
     }
     float tmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 16 * u + 4 * (lane / 16) + r;
-        const float v = t < row_limit ? s[u][r] * g.scale_log2 : -INFINITY;
+        const int j = 4 * (lane / 16) + r, t = t0 + 16 * u + j;
+        const bool ok = t < row_limit && ((T.kvalid[u] >> j) & 1);
+        const float v = ok ? s[u][r] * g.scale_log2 : -INFINITY;
         s[u][r] = v;
         tmax = fmaxf(tmax, v);
       }
@@ -177,13 +210,22 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
 #pragma unroll
       for (int r = 0; r < RP; ++r) pv[r] = pbuf[wave][tok][r];
       float vv[8];
-      unpack8(*reinterpret_cast<const u32x4*>(&vf[it]), vv);
+      unpack8(*reinterpret_cast<const u32x4*>(&T.v[it]), vv);
 #pragma unroll
       for (int r = 0; r < RP; ++r)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][e] = __builtin_fmaf(pv[r], vv[e], acc[r][e]);
     }
     wave_sync();  // pbuf / cbuf are rewritten by the next chunk
+  };
+
+  // The wave's chunks are first, first + 8, ... (issuing two chunks' loads before computing them, or prefetching
+  // the next chunk during the current one, measured no faster: a read-only kernel with this access pattern and
+  // no compute takes ~35 us where this one takes ~43 us for 163 MB of K/V).
+  for (int ch = tok_begin / kChunk + wave; ch < ch_end; ch += kWaves) {
+    Tile A;
+    load_tile(A, ch);
+    compute_tile(A, ch);
   }
 
   // sum the TPI token groups (lanes dg + LPT * ts) and the row sums (lanes qrow + 16 * j)
@@ -220,6 +262,41 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
         den = __builtin_fmaf(red_l[w][r], f, den);
       }
     }
+    if (g.splits > 1) {  // this block's record; merged by paged_decode_combine
+      float* rec = g.ws + ((int64_t(pair) * g.splits + split) * RP + r) * (2 + D);
+      if (d == 0) {
+        rec[0] = M;
+        rec[1] = den;
+      }
+      rec[2 + d] = num;
+      continue;
+    }
+    const float o = den > 0.0f ? num / den : 0.0f;
+    const int i = r / g.G, hh = r % g.G;
+    g.out[int64_t(b * g.q_len + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
+  }
+}
+
+// Merges the split records of one (sequence, kv head) in split order: O = sum_s O_s 2^(m_s - M) /
+// sum_s l_s 2^(m_s - M), M = max_s m_s; a row no split saw (M = -inf) is zero.
+template <int D, int RP>
+__global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) {
+  const int pair = blockIdx.x, b = pair / g.Hkv, kvh = pair % g.Hkv;
+  const int rows = g.G * g.q_len;
+  for (int idx = threadIdx.x; idx < rows * D; idx += 256) {
+    const int r = idx / D, d = idx % D;
+    const float* rec = g.ws + (int64_t(pair) * g.splits * RP + r) * (2 + D);
+    const int64_t step = int64_t(RP) * (2 + D);
+    float M = -INFINITY;
+    for (int sp = 0; sp < g.splits; ++sp) M = fmaxf(M, rec[sp * step]);
+    float num = 0.0f, den = 0.0f;
+    if (M != -INFINITY) {
+      for (int sp = 0; sp < g.splits; ++sp) {
+        const float f = exp2f(rec[sp * step] - M);
+        num = __builtin_fmaf(rec[sp * step + 2 + d], f, num);
+        den = __builtin_fmaf(rec[sp * step + 1], f, den);
+      }
+    }
     const float o = den > 0.0f ? num / den : 0.0f;
     const int i = r / g.G, hh = r % g.G;
     g.out[int64_t(b * g.q_len + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
@@ -228,10 +305,13 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
 
 template <int D, int RP>
 int launch_decode(const DecodeArgs& g, int64_t num_seqs, hipStream_t s) {
-  const dim3 grid(unsigned(num_seqs * g.Hkv)), block(kWaves * 64);
+  const dim3 grid(unsigned(num_seqs * g.Hkv * g.splits)), block(kWaves * 64);
   if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((paged_decode_kernel<D, RP, false>), grid, block, 0, s, g);
-  return check_launch("paged_decode_attention");
+  if (int rc = check_launch("paged_decode_attention")) return rc;
+  if (g.splits == 1) return NVHIP_OK;
+  hipLaunchKernelGGL((paged_decode_combine<D, RP>), dim3(unsigned(num_seqs * g.Hkv)), dim3(256), 0, s, g);
+  return check_launch("paged_decode_attention (combine)");
 }
 
 template <int D>
@@ -244,8 +324,40 @@ int launch_decode_rows(const DecodeArgs& g, int64_t num_seqs, int rows, hipStrea
   return invalid("paged_decode_attention: at most 8 query rows per kv head with head_dim 256");
 }
 
+int rows_padded(int64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16; }
+
+// Context split: only when there are fewer (sequence, kv head) pairs than CUs -- every extra block on a CU pays
+// the start-up latency of its first loads again (measured: 1 -> 2 -> 4 splits of a 32-sequence batch took 42 ->
+// 50 -> 56 us) -- aiming at ~256 blocks in splits of whole 256-token rounds (32 tokens per wave x 8 waves), the
+// longest possible context (max_blocks * block_size) setting the count.
+void split_policy(int64_t num_seqs, int64_t Hkv, int64_t max_ctx, int& splits, int& split_len) {
+  constexpr int64_t kRound = kChunk * kWaves, kTargetBlocks = 256;
+  const int64_t pairs = std::max<int64_t>(1, num_seqs * Hkv);
+  const int64_t want = std::max<int64_t>(1, (kTargetBlocks + pairs - 1) / pairs);
+  int64_t len = std::max<int64_t>(kRound, (max_ctx + want - 1) / want);
+  len = (len + kRound - 1) / kRound * kRound;
+  const int64_t n = std::max<int64_t>(1, (max_ctx + len - 1) / len);
+  splits = int(std::min<int64_t>(n, 1 << 16));
+  split_len = int(std::min<int64_t>(len, INT32_MAX / 2));
+}
+
+int64_t workspace_bytes(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_ctx) {
+  int splits, split_len;
+  split_policy(num_seqs, Hkv, max_ctx, splits, split_len);
+  if (splits <= 1) return 0;
+  return num_seqs * Hkv * splits * rows_padded((Hq / Hkv) * q_len) * (2 + D) * int64_t(sizeof(float));
+}
+
 }  // namespace
 }  // namespace nvhip
+
+extern "C" int64_t nvhip_paged_decode_attention_workspace_size(int64_t num_seqs, int64_t q_len, int64_t Hq,
+                                                               int64_t Hkv, int64_t D, int64_t block_size,
+                                                               int64_t max_blocks) {
+  if (num_seqs <= 0 || q_len < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || D < 1 || block_size < 1 || max_blocks < 0)
+    return 0;
+  return nvhip::workspace_bytes(num_seqs, q_len, Hq, Hkv, D, max_blocks * block_size);
+}
 
 extern "C" int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_cache, const void* v_cache,
                                                  const int32_t* block_table, const int32_t* context_lens,
@@ -253,7 +365,8 @@ extern "C" int nvhip_paged_decode_attention_bf16(void* out, const void* q, const
                                                  int64_t block_size, int64_t num_blocks, int64_t max_blocks,
                                                  int64_t q_stride_token, int64_t q_stride_head,
                                                  int64_t out_stride_token, int64_t out_stride_head, float scale,
-                                                 int causal, void* stream) {
+                                                 int causal, void* workspace, int64_t workspace_size,
+                                                 void* stream) {
   using namespace nvhip;
   clear_error();
   if (num_seqs < 0 || q_len < 1 || Hq < 1 || Hkv < 1 || block_size < 1 || num_blocks < 0 || max_blocks < 0)
@@ -290,7 +403,19 @@ extern "C" int nvhip_paged_decode_attention_bf16(void* out, const void* q, const
                out_stride_token,
                out_stride_head,
                scale * 1.4426950408889634f,
-               causal ? 1 : 0};
+               causal ? 1 : 0,
+               1,
+               int(max_blocks * block_size),
+               nullptr};
+  // split the context over several blocks when the caller gave a large enough workspace
+  const int64_t need = workspace_bytes(num_seqs, q_len, Hq, Hkv, D, max_blocks * block_size);
+  if (need > 0 && workspace && workspace_size >= need) {
+    if (reinterpret_cast<uintptr_t>(workspace) % alignof(float) != 0)
+      return invalid("paged_decode_attention: workspace must be 4-byte aligned");
+    split_policy(num_seqs, Hkv, max_blocks * block_size, g.splits, g.split_len);
+    g.ws = static_cast<float*>(workspace);
+  }
+  if (num_seqs * Hkv * g.splits > INT32_MAX) return invalid("paged_decode_attention: size too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (D) {
     case 64: return launch_decode_rows<64>(g, num_seqs, int(rows), s);

@@ -10,7 +10,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnvhip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 NVHIP_OK = 0
 NVHIP_EINVAL = -1
@@ -36,8 +36,10 @@ SIGNATURES = {
     "nvhip_silu_mul_bf16": [_p, _p, _i64, _i64, _i64, _p],
     "nvhip_matmul": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _p],
     "nvhip_paged_decode_attention_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                          _i64, _i64, _i64, _i64, _f, _i, _p],
+                                          _i64, _i64, _i64, _i64, _f, _i, _p, _i64, _p],
+    "nvhip_paged_decode_attention_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i64],
 }
+RESTYPES = {"nvhip_last_error": ctypes.c_char_p, "nvhip_paged_decode_attention_workspace_size": ctypes.c_int64}
 
 _lib = None
 
@@ -56,7 +58,7 @@ def lib() -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_char_p if name == "nvhip_last_error" else ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         version = handle.nvhip_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libnvhip.so ABI version {version}, expected {ABI_VERSION}: rebuild it")

@@ -165,12 +165,16 @@ def _matmul_fake(a, b, input_precision):
 def _paged_decode_attention_impl(q, k_cache, v_cache, block_table, context_lens, q_len, scale, causal):
     T, Hq, D = q.shape
     num_blocks, block_size, Hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    num_seqs, max_blocks = context_lens.shape[0], block_table.shape[1]
     out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
-    status = _lib.lib().nvhip_paged_decode_attention_bf16(
+    lib = _lib.lib()
+    ws_bytes = lib.nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, Hkv, D, block_size, max_blocks)
+    ws = torch.empty((max(ws_bytes, 0) + 3) // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    status = lib.nvhip_paged_decode_attention_bf16(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
-        context_lens.data_ptr(), context_lens.shape[0], q_len, Hq, Hkv, D, block_size, num_blocks,
-        block_table.shape[1], q.stride(0), q.stride(1), out.stride(0), out.stride(1), scale, int(causal),
-        _lib.stream_of(q))
+        context_lens.data_ptr(), num_seqs, q_len, Hq, Hkv, D, block_size, num_blocks, max_blocks,
+        q.stride(0), q.stride(1), out.stride(0), out.stride(1), scale, int(causal),
+        ws.data_ptr() if ws is not None else None, ws_bytes if ws is not None else 0, _lib.stream_of(q))
     _lib.check(status, "paged_decode_attention")
     return out
 

@@ -133,3 +133,35 @@ def test_rejects_bad_arguments():
     with pytest.raises(ValueError):   # 32 rows per kv head
         flash_attn_with_kvcache(q.repeat(1, 2, 1, 1), kc[:, :, :1].contiguous(), vc[:, :, :1].contiguous(), lens, bt,
                                 0.1, True)
+
+
+def _abi_call(q, kc, vc, lens, bt, scale, causal, workspace):
+    """Calls the C entry point directly: workspace None -> one block per (sequence, kv head); else split."""
+    from nanovllm_hip import _lib
+    num_seqs, q_len, Hq, D = q.shape
+    qf = q.reshape(num_seqs * q_len, Hq, D)
+    out = torch.empty_like(qf)
+    lib = _lib.lib()
+    need = lib.nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, kc.shape[2], D, kc.shape[1],
+                                                           bt.shape[1])
+    ws = torch.empty(max(need, 4) // 4 + 1, dtype=torch.float32, device=q.device) if workspace else None
+    status = lib.nvhip_paged_decode_attention_bf16(
+        out.data_ptr(), qf.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), lens.data_ptr(), num_seqs,
+        q_len, Hq, kc.shape[2], D, kc.shape[1], kc.shape[0], bt.shape[1], qf.stride(0), qf.stride(1),
+        out.stride(0), out.stride(1), scale, int(causal), ws.data_ptr() if ws is not None else None,
+        ws.numel() * 4 if ws is not None else 0, _lib.stream_of(q))
+    _lib.check(status, "paged_decode_attention")
+    return out.view(q.shape), need
+
+
+@pytest.mark.parametrize("lens", [[300, 2048, 1, 777, 256, 512, 0, 1500], [5000, 17, 4096]])
+def test_split_and_single_pass_agree_with_oracle(lens):
+    """The split-context path (workspace) and the one-block path (no workspace) both match the oracle."""
+    q, kc, vc, lt, bt = make_case(lens, seed=len(lens))
+    ref = oracle.paged_decode_attention(q, kc, vc, lt, bt, 0.1, True)
+    dev = [t.to(DEV) for t in (q, kc, vc, lt, bt)]
+    split, need = _abi_call(*dev, 0.1, True, workspace=True)
+    single, _ = _abi_call(*dev, 0.1, True, workspace=False)
+    assert need > 0
+    for out in (split, single):
+        torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=1.6e-2, atol=1e-2)
