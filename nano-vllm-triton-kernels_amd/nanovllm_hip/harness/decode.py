@@ -12,11 +12,12 @@ candidates there (a near-tie flipped by a last-bit difference has a tiny gap), t
 and the number of kernel nodes in each decode graph.
 
 The attention of the decode steps (shared by both backends) is the HIP paged decode attention by default
-(--attention torch: the harness's fp32 torch code).
+(--attention torch: the harness's fp32 torch code). The hip backend's projections and LM head use the HIP GEMM by
+default (--linear torch: torch's F.linear, as in the torch backend).
 
 Usage: python -m nanovllm_hip.harness.decode [--batch 32] [--steps 32] [--layers 28] [--min-len 512]
                                              [--max-len 2048] [--seed 0] [--reps 20] [--fp32-logits]
-                                             [--attention hip|torch]
+                                             [--attention hip|torch] [--linear hip|torch]
 """
 import argparse
 import ctypes
@@ -53,15 +54,15 @@ class Batch:
 
 
 @torch.inference_mode()
-def prefill(model, batch, backend, fp32_logits=False, reference=None):
+def prefill(model, batch, backend, fp32_logits=False, reference=None, linear="hip"):
     """Prefills every request; returns its first generated token (greedy) and, where it differs from
     reference[i], this backend's logit gap between its token and the reference's."""
     first, gaps = [], {}
     for i, prompt in enumerate(batch.prompts):
         n = len(prompt)
         ctx = Context(True, batch.slots(i, range(n)).to(batch.device))
-        h = model.forward(prompt.to(batch.device), torch.arange(n, device=batch.device), ctx, backend)
-        logits = model.logits(h[-1:], fp32_logits)[0]
+        h = model.forward(prompt.to(batch.device), torch.arange(n, device=batch.device), ctx, backend, linear=linear)
+        logits = model.logits(h[-1:], fp32_logits, backend, linear)[0]
         tok = int(logits.argmax())
         if reference is not None and reference[i] != tok:
             gaps[i] = {"step": "prefill", "logit_gap": round(float(logits[tok] - logits[reference[i]]), 5)}
@@ -72,9 +73,9 @@ def prefill(model, batch, backend, fp32_logits=False, reference=None):
 class DecodeStep:
     """Static input buffers of one decode step and the step itself (eager or replayed from a graph)."""
 
-    def __init__(self, model, batch, backend, fp32_logits=False, attention="hip"):
+    def __init__(self, model, batch, backend, fp32_logits=False, attention="hip", linear="hip"):
         self.model, self.batch, self.backend, self.fp32_logits = model, batch, backend, fp32_logits
-        self.attention = attention
+        self.attention, self.linear = attention, linear
         B, dev = len(batch.lens), batch.device
         self.input_ids = torch.zeros(B, dtype=torch.int64, device=dev)
         self.positions = torch.zeros(B, dtype=torch.int64, device=dev)
@@ -94,8 +95,8 @@ class DecodeStep:
 
     def forward(self):
         ctx = Context(False, self.slot_mapping, self.context_lens, self.batch.block_tables)
-        h = self.model.forward(self.input_ids, self.positions, ctx, self.backend, self.attention)
-        logits = self.model.logits(h, self.fp32_logits)
+        h = self.model.forward(self.input_ids, self.positions, ctx, self.backend, self.attention, self.linear)
+        logits = self.model.logits(h, self.fp32_logits, self.backend, self.linear)
         return logits, logits.argmax(dim=-1)
 
     def capture(self):
@@ -118,9 +119,10 @@ class DecodeStep:
 
 
 @torch.inference_mode()
-def decode(model, batch, first, steps, backend, use_graph, reference=None, fp32_logits=False, attention="hip"):
+def decode(model, batch, first, steps, backend, use_graph, reference=None, fp32_logits=False, attention="hip",
+           linear="hip"):
     """Greedy decode of `steps` tokens after `first`; returns (tokens [B][steps], divergence info vs reference)."""
-    step = DecodeStep(model, batch, backend, fp32_logits, attention)
+    step = DecodeStep(model, batch, backend, fp32_logits, attention, linear)
     if use_graph:
         step.set_inputs(first, 0)
         step.capture()
@@ -188,8 +190,10 @@ def main(argv=None):
     p.add_argument("--fp32-logits", action="store_true", help="LM head in fp32 (both backends)")
     p.add_argument("--attention", choices=("hip", "torch"), default="hip",
                    help="decode attention of both backends: HIP paged kernel or the fp32 torch code")
+    p.add_argument("--linear", choices=("hip", "torch"), default="hip",
+                   help="projections and LM head of the hip backend: HIP GEMM or torch F.linear")
     args = p.parse_args(argv)
-    f32, att = args.fp32_logits, args.attention
+    f32, att, lin = args.fp32_logits, args.attention, args.linear
     dev = torch.device("cuda:0")
     cfg = Qwen3Config(num_hidden_layers=args.layers)
     t0 = time.time()
@@ -198,17 +202,18 @@ def main(argv=None):
     out = {"config": {"model": "Qwen3-0.6B shapes, random init", "layers": args.layers, "batch": args.batch,
                       "steps": args.steps, "prompt_lens": [args.min_len, args.max_len], "kv_blocks": batch.num_blocks,
                       "block_size": BLOCK, "lm_head": "fp32" if f32 else "bf16",
-                      "decode_attention": att}}
+                      "decode_attention": att, "hip_backend_linear": lin}}
     print(f"model + batch ready in {time.time() - t0:.1f}s; prompts {sum(batch.lens)} tokens", flush=True)
 
     # hip backend: prefill, eager decode, graph decode from the same KV state
     cache = model.allocate_kv_cache(batch.num_blocks)
-    first_h, _ = prefill(model, batch, "hip", f32)
+    first_h, _ = prefill(model, batch, "hip", f32, linear=lin)
     snapshot = cache.clone()
-    tok_h, _, _ = decode(model, batch, first_h, args.steps, "hip", use_graph=False, fp32_logits=f32, attention=att)
+    tok_h, _, _ = decode(model, batch, first_h, args.steps, "hip", use_graph=False, fp32_logits=f32, attention=att,
+                         linear=lin)
     cache.copy_(snapshot)
     tok_hg, _, step_hg = decode(model, batch, first_h, args.steps, "hip", use_graph=True, fp32_logits=f32,
-                                attention=att)
+                                attention=att, linear=lin)
     print("hip backend done", flush=True)
     # torch backend (the reference): eager decode, compared step by step with the hip tokens (while a request's
     # history is identical its logits are directly comparable), then graph decode

@@ -8,8 +8,10 @@ backend "hip"   : rms_norm / fused_add_rms_norm_ (residual in place) / silu_and_
                   nanovllm_hip.kernels (the fused kernel does q/k norm, RoPE and the KV write in one launch).
 backend "torch" : the layers' own torch code run eagerly (what the reference's "compile" backend compiles), with
                   the unfused q_norm, k_norm, rotary and KV scatter.
-Both backends share everything else: the projections (torch F.linear), the embedding / tied LM head, and the
-attention, so that token differences between them come only from the four kernels. The attention is chosen apart
+The projections and the tied LM head use the HIP GEMM (nanovllm_hip.kernels.matmul, the wiring of linear.py:51,
+:73, :153 and embed_head.py:63) in the hip backend and torch's F.linear in the torch backend; forward(...,
+linear="torch") makes the hip backend use F.linear too, so that token differences come only from the four kernels.
+Both backends share the embedding and the attention. The attention is chosen apart
 from the backend: "torch" = the fp32 code below (prefill and decode), "hip" = the HIP paged decode attention
 (nanovllm_hip.kernels.attention, the flash_attn_with_kvcache call of layers/attention.py:84-90) for decode steps,
 the fp32 code for prefill.
@@ -128,6 +130,11 @@ def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scal
     return o.reshape(B, hq, d).to(q.dtype)
 
 
+def hip_linear(x, w):
+    """nn.Linear without bias through the HIP GEMM: x [T, in] @ w[out, in]^T (B = w.t(), the K-contiguous layout)."""
+    return hip.matmul(x, w.t())
+
+
 # ------------------------------------------------------------------ the model
 
 class Qwen3:
@@ -165,9 +172,11 @@ class Qwen3:
         self.kv = [(cache[0, i], cache[1, i]) for i in range(c.num_hidden_layers)]
         return cache
 
-    def forward(self, input_ids, positions, ctx: Context, backend: str, attention: str = "torch"):
+    def forward(self, input_ids, positions, ctx: Context, backend: str, attention: str = "torch",
+                linear: str = "hip"):
         """Returns the final hidden states [T, hidden] (after the last norm)."""
         c = self.cfg
+        lin = hip_linear if backend == "hip" and linear == "hip" else F.linear
         eps = c.rms_norm_eps
         hq, hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         h = F.embedding(input_ids, self.embed)
@@ -183,7 +192,7 @@ class Qwen3:
             else:
                 h, residual = add_rms_forward(h, residual, L["input_norm"], eps)
             # attention pre-segment: q/k/v are strided views of the qkv projection output
-            qkv = F.linear(h, L["qkv"])
+            qkv = lin(h, L["qkv"])
             q, k, v = qkv.split([hq * D, hkv * D, hkv * D], dim=-1)
             q, k, v = q.view(-1, hq, D), k.view(-1, hkv, D), v.view(-1, hkv, D)
             if backend == "hip":
@@ -205,27 +214,30 @@ class Qwen3:
                                             ctx.block_tables, self.scale, causal=True).view(-1, hq, D)
             else:
                 o = paged_decode_attention(q, k_cache, v_cache, ctx.block_tables, ctx.context_lens, self.scale)
-            h = F.linear(o.reshape(o.shape[0], hq * D), L["o"])
+            h = lin(o.reshape(o.shape[0], hq * D), L["o"])
             # post_attention_layernorm + MLP
             if backend == "hip":
                 h, residual = hip.fused_add_rms_norm_(h, residual, L["post_norm"], eps)
-                h = hip.silu_and_mul(F.linear(h, L["gate_up"]))
+                h = hip.silu_and_mul(lin(h, L["gate_up"]))
             else:
                 h, residual = add_rms_forward(h, residual, L["post_norm"], eps)
                 gate, up = F.linear(h, L["gate_up"]).chunk(2, -1)
                 h = F.silu(gate) * up
-            h = F.linear(h, L["down"])
+            h = lin(h, L["down"])
         if backend == "hip":
             h, _ = hip.fused_add_rms_norm_(h, residual, self.final_norm, eps)
         else:
             h, _ = add_rms_forward(h, residual, self.final_norm, eps)
         return h
 
-    def logits(self, h, fp32=False):
+    def logits(self, h, fp32=False, backend="torch", linear="hip"):
         """Tied LM head (embed_head.py:56-68): bf16 like the reference (then fp32 for sampling), or with fp32=True
-        the same product in fp32, which removes the exact ties of bf16-rounded logits."""
+        the same product in fp32, which removes the exact ties of bf16-rounded logits. The hip backend's bf16 head
+        is the HIP GEMM (unless linear="torch")."""
         if fp32:
             return F.linear(h.float(), self.embed.float())
+        if backend == "hip" and linear == "hip":
+            return hip_linear(h, self.embed).float()
         return F.linear(h, self.embed).float()
 
 
