@@ -11,7 +11,8 @@ One step = one launch over the T tokens. NSETS input/output sets (each with its 
 launch to launch so that the working set (> 256 MB) does not stay in the Infinity Cache; the K timed launches are
 replayed from HIP graphs and timed with HIP events on the stream they run on.
 
-Also reported (under "extra"): the same kernel at T = 1, 32, 2048; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
+Also reported (under "extra"): the same kernel at T = 1, 32, 2048; the unfused KV write (store_kvcache, bytes =
+T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
 the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s.
@@ -155,6 +156,14 @@ def extras(torch, oracle, kernels, dev, steps):
         ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, max(40, steps), 20)
         out[f"qk_norm_rope_kv_T{T}"] = {"us": round(ms * 1e3, 3),
                                         "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1)}
+    wl = FusedWorkload(8192, dev, torch, oracle, seed=5)
+    ms, _ = time_graph(torch, lambda i: kernels.store_kvcache(wl.sets[i % NSETS]["k"], wl.sets[i % NSETS]["v"],
+                                                              wl.k_cache, wl.v_cache, wl.sets[i % NSETS]["slots"]),
+                       NSETS, max(40, steps), 20)
+    nbytes = 8192 * (4 * HKV * D * 2 + 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out["store_kvcache_T8192"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    del wl
     T, H, I = 8192, 1024, 3072
     g = torch.Generator("cpu").manual_seed(2)
     xs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]

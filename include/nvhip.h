@@ -90,6 +90,18 @@ int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, int64_t N, in
                  int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype, int precision, void* stream);
 
 /*
+ * Paged KV-cache write (unfused).
+ * Replaces store_kvcache() of nanovllm/layers/attention.py:34-41 (its Triton kernel :11-31).
+ *   key, value: n rows of row_elems elements (Hkv * head_dim) at ptr + t*stride (elements contiguous).
+ *   k_cache, v_cache: [num_slots, row_elems] contiguous (blocks x block_size slots). Row t goes to slot
+ *   slot_mapping[t] (int32); slots outside [0, num_slots) (the padding value -1) are skipped.
+ *   elem_size: 2 (bf16 / fp16) or 4 (fp32) bytes; the bits are copied unchanged.
+ */
+int nvhip_store_kvcache(void* k_cache, void* v_cache, const void* key, const void* value, int64_t key_stride,
+                        int64_t value_stride, const int32_t* slot_mapping, int64_t num_slots, int64_t n,
+                        int64_t row_elems, int64_t elem_size, void* stream);
+
+/*
  * Paged decode attention over the KV cache that nvhip_qk_norm_rope_kv_bf16 writes.
  * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=context_lens, block_table=block_table,
  * softmax_scale=scale, causal=True) as called at nanovllm/layers/attention.py:84-90 (decode branch).

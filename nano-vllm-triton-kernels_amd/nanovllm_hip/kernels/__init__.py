@@ -6,6 +6,7 @@ dispatch on it ("hip" selects these kernels; "compile" keeps the layers' own tor
 from nanovllm_hip.kernels.matmul import matmul  # noqa: F401
 from nanovllm_hip.kernels.qk_norm_rope_kv import qk_norm_rope_kv  # noqa: F401
 from nanovllm_hip.kernels.rms_norm import fused_add_rms_norm, fused_add_rms_norm_, rms_norm  # noqa: F401
+from nanovllm_hip.kernels.store_kvcache import store_kvcache  # noqa: F401
 from nanovllm_hip.kernels.swiglu import silu_and_mul  # noqa: F401
 
 BACKENDS = ("compile", "hip")

@@ -22,6 +22,8 @@ _DEF.define("fused_add_rms_norm(Tensor x, Tensor residual, Tensor w, float eps) 
 _DEF.define("fused_add_rms_norm_(Tensor x, Tensor(a!) residual, Tensor w, float eps) -> Tensor")
 _DEF.define("silu_and_mul(Tensor x) -> Tensor")
 _DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
+_DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+            "Tensor slot_mapping) -> ()")
 _DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
             "Tensor context_lens, int q_len, float scale, bool causal) -> Tensor")
 
@@ -185,3 +187,22 @@ _DEF.impl("paged_decode_attention", _paged_decode_attention_impl, "CUDA")
 @torch.library.register_fake("nvhip::paged_decode_attention")
 def _paged_decode_attention_fake(q, k_cache, v_cache, block_table, context_lens, q_len, scale, causal):
     return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+
+
+# ------------------------------------------------------------------ store_kvcache
+
+def _store_kvcache_impl(key, value, k_cache, v_cache, slot_mapping):
+    n, row = key.shape[0], key.shape[1] * key.shape[2]
+    num_slots = k_cache.numel() // row if row else 0
+    status = _lib.lib().nvhip_store_kvcache(k_cache.data_ptr(), v_cache.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                            key.stride(0), value.stride(0), slot_mapping.data_ptr(), num_slots, n,
+                                            row, key.element_size(), _lib.stream_of(key))
+    _lib.check(status, "store_kvcache")
+
+
+_DEF.impl("store_kvcache", _store_kvcache_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::store_kvcache")
+def _store_kvcache_fake(key, value, k_cache, v_cache, slot_mapping):
+    return None
