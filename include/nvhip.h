@@ -90,6 +90,17 @@ int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, int64_t N, in
                  int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype, int precision, void* stream);
 
 /*
+ * GEMM with the SiLU x Mul epilogue (the gate_up projection of an MLP and its activation in one launch):
+ * out[M, N2] = bf16(bf16(silu(bf16(A Wg^T))) * bf16(A Wu^T)), W = [Wg; Wu] of shape [2*N2, K] (an nn.Linear
+ * gate_up weight), fp32 accumulation; bitwise nvhip_silu_mul_bf16 applied to the nvhip_matmul result.
+ * Not in the reference's kernels (its matmul.py:3-4 plans this epilogue as the next step).
+ *   A [M, K] bf16 row stride sam; W row stride swn (K-contiguous rows, K % 8 == 0, 16-byte aligned rows);
+ *   out row stride som (elements contiguous).
+ */
+int nvhip_matmul_silu_mul_bf16(void* out, const void* a, const void* w, int64_t M, int64_t N2, int64_t K,
+                               int64_t sam, int64_t swn, int64_t som, void* stream);
+
+/*
  * Paged KV-cache write (unfused).
  * Replaces store_kvcache() of nanovllm/layers/attention.py:34-41 (its Triton kernel :11-31).
  *   key, value: n rows of row_elems elements (Hkv * head_dim) at ptr + t*stride (elements contiguous).

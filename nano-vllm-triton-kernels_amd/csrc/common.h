@@ -44,6 +44,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float a) { return uint16_t(pack_
 // fp32 value rounded to the nearest bf16 (as an fp32): the .to(torch.bfloat16) of the torch code.
 __device__ __forceinline__ float round_bf16(float a) { return bf16_lo(pack_bf16x2(a, 0.0f)); }
 
+// silu(g) = g / (1 + exp(-g)) rounded to bf16: torch's own silu kernel formula (device expf, correctly rounded
+// divide) on a bf16 input, as F.silu(gate) of layers/activation.py:15-18 computes it. Shared by the SiLU x Mul kernel
+// and the GEMM epilogue that fuses it, so both give the same bits.
+__device__ __forceinline__ float silu_bf16(float g) { return round_bf16(g / (1.0f + expf(-g))); }
+
 // 8 bf16 (16 bytes) <-> 8 fp32.
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 #pragma unroll

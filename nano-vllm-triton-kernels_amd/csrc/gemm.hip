@@ -156,7 +156,10 @@ __device__ __forceinline__ void tile_coords(int pid, int M, int N, int BM, int B
   pid_n = (pid % in_group) / group_rows;
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL>
+// SILU: W is [2 * N2, K] = [gate; up] (N = 2 * N2) and C is [M, N2] = bf16(silu(A Wg^T)) * bf16(A Wu^T) rounded
+// to bf16: a tile's first BN / 2 B rows are gate rows n0 / 2 .., the last BN / 2 the matching up rows N2 + n0 / 2 ..
+// (so the per-column k order is that of the plain product, and the result is bitwise the unfused one).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const MfmaArgs g) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
@@ -186,8 +189,12 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   for (int i = 0; i < CH; ++i) {
     const bool isA = i < AC;
     const int c = tid + NT * (isA ? i : i - AC), row = c / 8, kc = c % 8;
-    src[i] = isA ? g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + kc * 8
-                 : g.w + int64_t(min(n0 + row, g.N - 1)) * g.swn + kc * 8;
+    int wrow = min(n0 + row, g.N - 1);
+    if constexpr (SILU) {
+      const int n2 = g.N / 2, half = BN / 2;
+      wrow = row < half ? min(n0 / 2 + row, n2 - 1) : n2 + min(n0 / 2 + row - half, n2 - 1);
+    }
+    src[i] = isA ? g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + kc * 8 : g.w + int64_t(wrow) * g.swn + kc * 8;
     dst[i] = (isA ? 0 : BM * kBK) + row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
     kofs[i] = kc * 8;
   }
@@ -287,6 +294,30 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
                   pack_bf16x2(acc[i][j][4 * run + 2], acc[i][j][4 * run + 3])};
       }
   __syncthreads();
+  if constexpr (SILU) {  // out[m][n0/2 + j] = bf16(silu(gate) * up), gate = column j, up = column j + BN/2
+    constexpr int HALF = BN / 2, CPR = HALF / 8;
+    const int n2 = g.N / 2;
+    for (int c = tid; c < BM * CPR; c += NT) {
+      const int rr = c / CPR, cc = (c % CPR) * 8;
+      const int m = m0 + rr, n = n0 / 2 + cc;
+      if (m >= g.M) continue;
+      const u32x4 gv = *reinterpret_cast<const u32x4*>(&ot[rr * OUT_PITCH + cc]);
+      const u32x4 uv = *reinterpret_cast<const u32x4*>(&ot[rr * OUT_PITCH + HALF + cc]);
+      float gf[8], uf[8], o[8];
+      unpack8(gv, gf);
+      unpack8(uv, uf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = silu_bf16(gf[e]) * uf[e];
+      const u32x4 v = pack8(o);
+      uint16_t* d = g.c + int64_t(m) * g.scm + n;
+      if (n + 8 <= n2 && (reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+        *reinterpret_cast<u32x4*>(d) = v;
+      } else {
+        for (int e = 0; e < 8 && n + e < n2; ++e) d[e] = uint16_t(v[e / 2] >> (16 * (e & 1)));
+      }
+    }
+    return;
+  }
   constexpr int CPR = BN / 8;  // 16-byte chunks per output row
   for (int c = tid; c < BM * CPR; c += NT) {
     const int rr = c / CPR, cc = (c % CPR) * 8;
@@ -310,48 +341,69 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
 // and the W rows; W is read once, A is small and stays in L2), U steps of loads issued before their MFMAs. The
 // NW partial 16-row tiles are summed through LDS in wave order (deterministic), rounded to bf16 and stored.
 
-template <int MT, int NW, int U>
+// SILU: W = [gate; up] ([2 * N2, K], N = 2 * N2), C [M, N2]: the block takes gate rows n0 .. and up rows N2 + n0 ..
+// and stores bf16(silu(gate) * up) of the two rounded sums (bitwise the unfused result).
+template <int MT, int NW, int U, bool SILU = false>
 __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
-  __shared__ float red[NW][MT][4][64];
+  constexpr int NP = SILU ? 2 : 1;  // products per block: (gate, up) or the plain one
+  __shared__ float red[NW][NP][MT][4][64];
   const int n0 = blockIdx.x * 16;
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int fr = lane % 16, fk = (lane / 16) * 8;
-  const uint16_t* wrow = g.w + int64_t(min(n0 + fr, g.N - 1)) * g.swn + fk;
+  const int nout = SILU ? g.N / 2 : g.N;
+  const uint16_t* wrows[NP];
+  wrows[0] = g.w + int64_t(min(n0 + fr, nout - 1)) * g.swn + fk;
+  if constexpr (SILU) wrows[NP - 1] = g.w + int64_t(nout + min(n0 + fr, nout - 1)) * g.swn + fk;
   const uint16_t* arow[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) arow[t] = g.a + int64_t(min(t * 16 + fr, g.M - 1)) * g.sam + fk;
-  f32x4_t acc[MT];
+  f32x4_t acc[NP][MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{};
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[p][t] = f32x4_t{};
   const int nks = (g.K + 31) / 32;
   for (int s0 = wave; s0 < nks; s0 += NW * U) {
-    bf16x8_t wf[U], af[U][MT];
+    bf16x8_t wf[U][NP], af[U][MT];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int ks = s0 + u * NW, k = ks * 32;
       const bool in = ks < nks && k + fk < g.K;  // K % 8 == 0: a lane's 8 values are all in or all out
-      wf[u] = in ? *reinterpret_cast<const bf16x8_t*>(wrow + k) : bf16x8_t{};
+#pragma unroll
+      for (int p = 0; p < NP; ++p) wf[u][p] = in ? *reinterpret_cast<const bf16x8_t*>(wrows[p] + k) : bf16x8_t{};
 #pragma unroll
       for (int t = 0; t < MT; ++t) af[u][t] = in ? *reinterpret_cast<const bf16x8_t*>(arow[t] + k) : bf16x8_t{};
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[u][t], wf[u], acc[t], 0, 0, 0);
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          acc[p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[u][t], wf[u][p], acc[p][t], 0, 0, 0);
   }
   // lane l, register r of tile t holds C row t*16 + 4*(l/16) + r, column n0 + l%16
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int p = 0; p < NP; ++p)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][p][t][r][lane] = acc[p][t][r];
   __syncthreads();
   for (int idx = threadIdx.x; idx < MT * 256; idx += NW * 64) {
     const int t = idx / 256, r = (idx / 64) % 4, l = idx % 64;
-    float sum = 0.0f;
+    float sum[NP];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) sum += red[w][t][r][l];
+    for (int p = 0; p < NP; ++p) {
+      sum[p] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum[p] += red[w][p][t][r][l];
+    }
     const int m = t * 16 + 4 * (l / 16) + r, n = n0 + l % 16;
-    if (m < g.M && n < g.N) g.c[int64_t(m) * g.scm + n] = f32_to_bf16(sum);
+    if (m >= g.M || n >= nout) continue;
+    float o = sum[0];
+    if constexpr (SILU) o = silu_bf16(round_bf16(sum[0])) * round_bf16(sum[1]);
+    g.c[int64_t(m) * g.scm + n] = f32_to_bf16(o);
   }
 }
 
@@ -484,45 +536,47 @@ __global__ __launch_bounds__(256) void gemm_mfma_f32(const F32Args g) {
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU>
 int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   const int64_t tiles = int64_t((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   if (tiles > INT32_MAX) return invalid("matmul: matrix too large");
-  hipLaunchKernelGGL((gemm_mfma_nt<BM, BN, WAVES_M, WAVES_N, RS, KTAIL>), dim3(unsigned(tiles)),
+  hipLaunchKernelGGL((gemm_mfma_nt<BM, BN, WAVES_M, WAVES_N, RS, KTAIL, SILU>), dim3(unsigned(tiles)),
                      dim3(WAVES_M * WAVES_N * 64), 0, s, g);
   return check_launch("matmul");
 }
 
 // Tile shape by output size (measured on MI355X at the Qwen3-0.6B projections, M = 2048): the largest tile that
 // still gives >= 192 tiles (3/4 of the 256 CUs); 64x64 tiles for 32 < M <= 64.
-template <int RS, bool KTAIL>
+template <int RS, bool KTAIL, bool SILU>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
-  if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL>(g, s);
-  if (tiles(256, 256) >= 192) return launch_mfma<256, 256, 4, 2, 1, KTAIL>(g, s);
-  if (tiles(128, 256) >= 192) return launch_mfma<128, 256, 2, 2, RS, KTAIL>(g, s);
-  if (tiles(128, 128) >= 192) return launch_mfma<128, 128, 2, 4, RS, KTAIL>(g, s);
-  return launch_mfma<128, 64, 2, 2, RS, KTAIL>(g, s);
+  if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU>(g, s);
+  if (tiles(256, 256) >= 192) return launch_mfma<256, 256, 4, 2, 1, KTAIL, SILU>(g, s);
+  if (tiles(128, 256) >= 192) return launch_mfma<128, 256, 2, 2, RS, KTAIL, SILU>(g, s);
+  if (tiles(128, 128) >= 192) return launch_mfma<128, 128, 2, 4, RS, KTAIL, SILU>(g, s);
+  return launch_mfma<128, 64, 2, 2, RS, KTAIL, SILU>(g, s);
 }
 
 // 8 waves per block; 4 k steps of loads per wave in flight for wide outputs, 8 when N < 2048 (fewer blocks, each
 // with more of W to stream) -- the best of a sweep over 4/8/16 waves and 2/4/8 steps at the Qwen3-0.6B shapes.
-template <int MT>
+template <int MT, bool SILU>
 int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   constexpr int NW = 8;
-  const dim3 grid(unsigned((g.N + 15) / 16)), block(NW * 64);
-  if (g.N >= 2048) hipLaunchKernelGGL((gemm_skinny<MT, NW, 4>), grid, block, 0, s, g);
-  else hipLaunchKernelGGL((gemm_skinny<MT, NW, 8>), grid, block, 0, s, g);
+  const int nout = SILU ? g.N / 2 : g.N;
+  const dim3 grid(unsigned((nout + 15) / 16)), block(NW * 64);
+  if (g.N >= 2048) hipLaunchKernelGGL((gemm_skinny<MT, NW, 4, SILU>), grid, block, 0, s, g);
+  else hipLaunchKernelGGL((gemm_skinny<MT, NW, 8, SILU>), grid, block, 0, s, g);
   return check_launch("matmul");
 }
 
+template <bool SILU>
 int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
-  if (g.M <= 16) return launch_skinny<1>(g, s);
-  if (g.M <= 32) return launch_skinny<2>(g, s);
+  if (g.M <= 16) return launch_skinny<1, SILU>(g, s);
+  if (g.M <= 32) return launch_skinny<2, SILU>(g, s);
   const int nk = (g.K + kBK - 1) / kBK;
-  if (g.K % kBK != 0) return launch_mfma_shape<1, true>(g, s);
-  if (nk % 2 == 0) return launch_mfma_shape<2, false>(g, s);
-  return launch_mfma_shape<1, false>(g, s);
+  if (g.K % kBK != 0) return launch_mfma_shape<1, true, SILU>(g, s);
+  if (nk % 2 == 0) return launch_mfma_shape<2, false, SILU>(g, s);
+  return launch_mfma_shape<1, false, SILU>(g, s);
 }
 
 template <bool B_NMAJOR, bool TF32>
@@ -566,7 +620,7 @@ extern "C" int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, in
     if (nt) {
       MfmaArgs m{static_cast<uint16_t*>(c), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
                  int(M), int(N), int(K), sam, sbn, scm};
-      return launch_mfma_auto(m, s);
+      return launch_mfma_auto<false>(m, s);
     }
     return launch_generic<uint16_t, false>(g, s);
   }
@@ -584,4 +638,21 @@ extern "C" int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, in
   }
   if (tf32) return launch_generic<float, true>(g, s);
   return launch_generic<float, false>(g, s);
+}
+
+extern "C" int nvhip_matmul_silu_mul_bf16(void* out, const void* a, const void* w, int64_t M, int64_t N2, int64_t K,
+                                          int64_t sam, int64_t swn, int64_t som, void* stream) {
+  using namespace nvhip;
+  clear_error();
+  if (M < 0 || N2 < 0 || K < 0) return invalid("matmul_silu_mul: negative size");
+  if (M == 0 || N2 == 0) return NVHIP_OK;
+  if (!out || !a || !w) return invalid("matmul_silu_mul: null pointer");
+  if (K <= 0 || K % 8 != 0 || sam % 8 != 0 || swn % 8 != 0 || sam < K || swn < K || som < N2 || !aligned16(a) ||
+      !aligned16(w))
+    return invalid("matmul_silu_mul: needs K % 8 == 0 and 16-byte aligned, K-contiguous rows of A and W");
+  if (M >= (int64_t(1) << 31) || 2 * N2 >= (int64_t(1) << 31) || K >= (int64_t(1) << 31))
+    return invalid("matmul_silu_mul: size too large");
+  MfmaArgs m{static_cast<uint16_t*>(out), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(w),
+             int(M), int(2 * N2), int(K), sam, swn, som};
+  return launch_mfma_auto<true>(m, static_cast<hipStream_t>(stream));
 }

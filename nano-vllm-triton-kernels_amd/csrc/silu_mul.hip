@@ -36,7 +36,6 @@ struct SiluArgs {
   FastDiv per_row;
 };
 
-__device__ __forceinline__ float silu_bf16(float g) { return round_bf16(g / (1.0f + expf(-g))); }
 
 __global__ __launch_bounds__(kBlock) void silu_mul_kernel(const SiluArgs a) {
   const uint32_t base = blockIdx.x * (kBlock * kVpt) + threadIdx.x;

@@ -9,8 +9,9 @@ backend "hip"   : rms_norm / fused_add_rms_norm_ (residual in place) / silu_and_
 backend "torch" : the layers' own torch code run eagerly (what the reference's "compile" backend compiles), with
                   the unfused q_norm, k_norm, rotary and KV scatter.
 The projections and the tied LM head use the HIP GEMM (nanovllm_hip.kernels.matmul, the wiring of linear.py:51,
-:73, :153 and embed_head.py:63) in the hip backend and torch's F.linear in the torch backend; forward(...,
-linear="torch") makes the hip backend use F.linear too, so that token differences come only from the four kernels.
+:73, :153 and embed_head.py:63; gate_up with the SiLU x Mul epilogue, matmul_silu_and_mul) in the hip backend and
+torch's F.linear in the torch backend; forward(..., linear="torch") makes the hip backend use F.linear and the
+separate silu_and_mul, so that token differences come only from the four kernels.
 Both backends share the embedding and the attention. The attention is chosen apart
 from the backend: "torch" = the fp32 code below (prefill and decode), "hip" = the HIP paged decode attention
 (nanovllm_hip.kernels.attention, the flash_attn_with_kvcache call of layers/attention.py:84-90) for decode steps,
@@ -218,7 +219,10 @@ class Qwen3:
             # post_attention_layernorm + MLP
             if backend == "hip":
                 h, residual = hip.fused_add_rms_norm_(h, residual, L["post_norm"], eps)
-                h = hip.silu_and_mul(lin(h, L["gate_up"]))
+                if linear == "hip":   # gate_up projection and SiLU x Mul in one launch (bitwise the two-step result)
+                    h = hip.matmul_silu_and_mul(h, L["gate_up"])
+                else:
+                    h = hip.silu_and_mul(lin(h, L["gate_up"]))
             else:
                 h, residual = add_rms_forward(h, residual, L["post_norm"], eps)
                 gate, up = F.linear(h, L["gate_up"]).chunk(2, -1)

@@ -22,6 +22,7 @@ _DEF.define("fused_add_rms_norm(Tensor x, Tensor residual, Tensor w, float eps) 
 _DEF.define("fused_add_rms_norm_(Tensor x, Tensor(a!) residual, Tensor w, float eps) -> Tensor")
 _DEF.define("silu_and_mul(Tensor x) -> Tensor")
 _DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
+_DEF.define("matmul_silu_mul(Tensor a, Tensor w) -> Tensor")
 _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
             "Tensor slot_mapping) -> ()")
 _DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
@@ -206,3 +207,23 @@ _DEF.impl("store_kvcache", _store_kvcache_impl, "CUDA")
 @torch.library.register_fake("nvhip::store_kvcache")
 def _store_kvcache_fake(key, value, k_cache, v_cache, slot_mapping):
     return None
+
+
+# ------------------------------------------------------------------ GEMM + SiLU x Mul epilogue
+
+def _matmul_silu_mul_impl(a, w):
+    M, K = a.shape
+    N2 = w.shape[0] // 2
+    out = torch.empty((M, N2), dtype=a.dtype, device=a.device)
+    status = _lib.lib().nvhip_matmul_silu_mul_bf16(out.data_ptr(), a.data_ptr(), w.data_ptr(), M, N2, K, a.stride(0),
+                                                   w.stride(0), out.stride(0), _lib.stream_of(a))
+    _lib.check(status, "matmul_silu_mul")
+    return out
+
+
+_DEF.impl("matmul_silu_mul", _matmul_silu_mul_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::matmul_silu_mul")
+def _matmul_silu_mul_fake(a, w):
+    return torch.empty((a.shape[0], w.shape[0] // 2), dtype=a.dtype, device=a.device)

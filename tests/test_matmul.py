@@ -113,3 +113,21 @@ def test_golden_small():
         wb = torch.from_numpy(z[f"w_bf16_{M}_{N}_{K}"].astype(np.int16)).view(torch.bfloat16).to(DEV)
         refb = torch.from_numpy(z[f"cb_f64_{M}_{N}_{K}"])
         torch.testing.assert_close(matmul(ab, wb.t()).cpu().double(), refb, rtol=1.6e-2, atol=1e-2 * math.sqrt(K))
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 32, 33, 64, 100, 2048])
+@pytest.mark.parametrize("I,K", [(3072, 1024), (40, 64), (300, 136)])
+def test_matmul_silu_mul_is_bitwise_the_two_step_result(M, I, K):
+    """The fused gate_up + SiLU x Mul equals silu_and_mul(matmul(x, w.t())) bit for bit (same per-column k order,
+    same rounding points); the two-step result itself is checked against the oracle elsewhere."""
+    from nanovllm_hip.kernels import matmul_silu_and_mul, silu_and_mul
+    g = torch.Generator("cpu").manual_seed(M * 7 + I)
+    x = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    w = torch.randn(2 * I, K, generator=g).to(torch.bfloat16).to(DEV)
+    fused = matmul_silu_and_mul(x, w)
+    two_step = silu_and_mul(matmul(x, w.t()))
+    assert fused.shape == (M, I)
+    assert torch.equal(fused, two_step)
+    # and against the oracle composition (float64 product rounded to bf16, then the reference's silu * up)
+    ref = oracle.silu_and_mul(oracle.matmul_fp64(x.cpu(), w.cpu().t()).to(torch.bfloat16))
+    torch.testing.assert_close(fused.cpu().float(), ref.float(), rtol=1.6e-2, atol=2e-2)
