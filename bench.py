@@ -15,7 +15,8 @@ Also reported (under "extra"): the same kernel at T = 1, 32, 2048; the unfused K
 T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
-the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s.
+the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s; the causal
+prefill attention of one layer over 4 sequences of 2048 tokens, in TFLOP/s.
 The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
 sample of the same workload.
 
@@ -208,6 +209,7 @@ def extras(torch, oracle, kernels, dev, steps):
                                          "torch_linear_us": round(ms_ref * 1e3, 2)}
         del a, w0, ws
     out["paged_decode_attention_B32"] = decode_attention(torch, dev, steps, g)
+    out["prefill_attention_4x2048"] = prefill_attention(torch, dev, steps, g)
     n = 4096
     a = torch.randn(n, n, generator=g).to(dev)
     b = torch.randn(n, n, generator=g).to(dev)
@@ -249,6 +251,23 @@ def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
     del sets
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "context_tokens": ctx, "bytes": nbytes}
+
+
+def prefill_attention(torch, dev, steps, g, nseq=4, L=2048):
+    """Causal prefill attention of one Qwen3-0.6B layer over nseq sequences of L tokens (k, v views of the qkv
+    output). flops = 4 * D * Hq * sum over queries of the keys each sees (L (L + 1) / 2 per sequence)."""
+    from nanovllm_hip.kernels.attention import flash_attn_varlen_func
+    T = nseq * L
+    buf = torch.randn(T, (HQ + 2 * HKV) * D + PAD, generator=g).to(torch.bfloat16).to(dev)
+    q = buf[:, :HQ * D].view(T, HQ, D)
+    k = buf[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D)
+    v = buf[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].view(T, HKV, D)
+    cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=dev)
+    ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True), 4,
+                       max(20, steps // 4), 4)
+    flops = 4 * D * HQ * nseq * L * (L + 1) // 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
 def copy_ceiling(torch, dev, mib=1024, reps=20):

@@ -1,0 +1,262 @@
+// Prefill (variable-length, causal) attention for gfx950.
+//
+// Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale,
+// causal=True, block_table) as nano-vllm calls it for prefill (layers/attention.py:77-83): sequence b owns query
+// tokens cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1 of q [Tq, Hq, D] and key tokens 0 .. lk-1, lk = cu_seqlens_k[b+1] -
+// cu_seqlens_k[b]; the keys are rows cu_seqlens_k[b] + j of k, v [Tk, Hkv, D], or, with a block table (prefix
+// cache, model_runner.py:311-312), cache slot block_table[b][j / block_size] * block_size + j % block_size of the
+// paged caches [num_blocks, block_size, Hkv, D]. Query i of a sequence with lq queries sees keys j <= lk - lq + i
+// with causal (the mask aligned to the bottom right), all lk keys otherwise. Head h reads kv head h / (Hq / Hkv).
+//
+// One block (4 waves) per (64-query tile, sequence, q head); wave w owns queries 16w .. 16w+15 of the tile. Per
+// 64-key tile:
+//   1. the K tile goes to LDS key-major ([64][D], 16-byte chunks, rows padded), the V tile dim-major ([D][64],
+//      transposed on the way in, so that a lane's keys of one dim are contiguous);
+//   2. S^T [16 keys x 16 queries] = K Q^T per 16-key subtile with v_mfma_f32_16x16x32_bf16 (K rows from LDS as the
+//      A operand, the wave's Q rows from registers as the B operand): lane l holds keys 4 (l / 16) + r of query
+//      l % 16;
+//   3. fp32 online softmax in base 2 (scale * log2 e folded in) per query (a 4-register max and two lane swaps);
+//   4. O^T [16 dims x 16 queries] += V^T P^T per 16-dim tile and 32-key step: P (bf16) stays in the registers it was
+//      computed in as the B operand, whose 8 k slots of lane l are the keys 4 (l / 16) .. +3 and 16 + 4 (l / 16) ..
+//      +3 of the step; the A operand reads the same keys of dim l % 16 from the transposed V tile (two 8-byte LDS
+//      reads). Each lane keeps one query's O, so the rescale by 2^(m_old - m_new) is lane-local.
+// P is rounded to bf16 for the P.V product (as flash-attn does); scores, softmax and O are fp32; output bf16.
+#include <algorithm>
+
+#include "common.h"
+
+namespace nvhip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kBQ = 64;   // queries per block
+constexpr int kBK = 64;   // keys per tile
+constexpr int kThreads = 256;
+
+struct PrefillArgs {
+  uint16_t* out;
+  const uint16_t* q;
+  const uint16_t* k;  // contiguous [Tk, Hkv, D] rows, or the k cache with a block table
+  const uint16_t* v;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* bt;  // [num_seqs, max_blocks] or null
+  int64_t q_st, q_sh, k_st, v_st, o_st, o_sh;
+  int Hkv, G, bs, num_blocks, max_blocks;
+  float scale_log2;
+  int causal;
+};
+
+// Element offset of key j of sequence b, kv head kvh, in k (v with v_st) -- or -1 if its cache block is invalid.
+template <int D>
+__device__ __forceinline__ int64_t key_row(const PrefillArgs& g, int b, int k0s, int j, int kvh, int64_t st) {
+  if (g.bt == nullptr) return int64_t(k0s + j) * st + int64_t(kvh) * D;
+  const int blk = g.bt[int64_t(b) * g.max_blocks + j / g.bs];
+  if (blk < 0 || blk >= g.num_blocks) return -1;
+  return ((int64_t(blk) * g.bs + j % g.bs) * g.Hkv + kvh) * D;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const PrefillArgs g) {
+  constexpr int KC = D / 32;   // 32-wide dim steps of Q.K
+  constexpr int DT = D / 16;   // 16-dim output tiles
+  constexpr int CPR = D / 8;   // 16-byte chunks per K/V row
+  constexpr int KP = D + 8;    // K row pitch (elements)
+  constexpr int VP = kBK + 8;  // V^T row pitch
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
+
+  const int qt = blockIdx.x, b = blockIdx.y, h = blockIdx.z, kvh = h / g.G;
+  const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
+  const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
+  if (qt * kBQ >= lq || lk <= 0) {
+    if (qt * kBQ < lq && threadIdx.x < kBQ && qt * kBQ + int(threadIdx.x) < lq) {  // no keys: zero rows
+      uint16_t* o = g.out + int64_t(q0s + qt * kBQ + threadIdx.x) * g.o_st + int64_t(h) * g.o_sh;
+      for (int d = 0; d < D; ++d) o[d] = 0;
+    }
+    return;
+  }
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int qi_lane = qt * kBQ + 16 * wave + lane % 16;  // this lane's query (B operand row / O column)
+  const int g4 = lane / 16;
+
+  // Q rows of the wave as the B operand: lane l -> query 16 wave + l % 16, dims 32c + 8 (l / 16) .. +8
+  bf16x8_t qf[KC];
+  {
+    const bool ok = qi_lane < lq;
+    const uint16_t* qp = g.q + int64_t(q0s + (ok ? qi_lane : 0)) * g.q_st + int64_t(h) * g.q_sh + 8 * g4;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) qf[c] = ok ? *reinterpret_cast<const bf16x8_t*>(qp + 32 * c) : bf16x8_t{};
+  }
+  const int diag = lk - lq;  // query i sees keys <= diag + i
+  const int q_last = min(qt * kBQ + kBQ, lq) - 1;
+  const int k_end = g.causal ? min(lk, diag + q_last + 1) : lk;  // keys this block needs
+  const int limit_lane = g.causal ? diag + qi_lane : lk - 1;      // last key of this lane's query
+
+  f32x4_t o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f32x4_t{0, 0, 0, 0};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  for (int kt0 = 0; kt0 < k_end; kt0 += kBK) {
+    // 1. K tile key-major: chunk c -> key c / CPR, dims (c % CPR) * 8; V tile: chunk c -> key c % 64, dims
+    // (c / 64) * 8, written transposed (lanes of a wave take consecutive keys of one dim chunk)
+    for (int c = tid; c < kBK * CPR; c += kThreads) {
+      const int key = c / CPR, dc = (c % CPR) * 8, j = kt0 + key;
+      u32x4 x = u32x4{0, 0, 0, 0};
+      if (j < lk) {
+        const int64_t row = key_row<D>(g, b, k0s, j, kvh, g.k_st);
+        if (row >= 0) x = *reinterpret_cast<const u32x4*>(g.k + row + dc);
+      }
+      *reinterpret_cast<u32x4*>(&Ks[key * KP + dc]) = x;
+    }
+    for (int c = tid; c < kBK * CPR; c += kThreads) {
+      const int key = c % kBK, dc = (c / kBK) * 8, j = kt0 + key;
+      u32x4 x = u32x4{0, 0, 0, 0};
+      if (j < lk) {
+        const int64_t row = key_row<D>(g, b, k0s, j, kvh, g.v_st);
+        if (row >= 0) x = *reinterpret_cast<const u32x4*>(g.v + row + dc);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[(dc + e) * VP + key] = uint16_t(x[e / 2] >> (16 * (e & 1)));
+    }
+    __syncthreads();
+
+    // 2. S^T per 16-key subtile: lane holds keys kt0 + 16 st + 4 g4 + r of query qi_lane
+    f32x4_t s[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      s[st] = f32x4_t{0, 0, 0, 0};
+      const uint16_t* kr = &Ks[(16 * st + lane % 16) * KP + 8 * g4];
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+        s[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(kr + 32 * c), qf[c], s[st],
+                                                        0, 0, 0);
+    }
+    // 3. online softmax of query qi_lane over this tile
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = kt0 + 16 * st + 4 * g4 + r;
+        const float v = (j < lk && j <= limit_lane) ? s[st][r] * g.scale_log2 : -INFINITY;
+        s[st][r] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    // p as bf16, packed per 32-key step in the k-slot order of the P.V product
+    bf16x8_t pf[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      float p[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = exp2f(s[2 * m][r] - m_use);
+        p[4 + r] = exp2f(s[2 * m + 1][r] - m_use);
+      }
+      const u32x4 pk = pack8(p);
+      float pr[8];
+      unpack8(pk, pr);  // the sum uses the bf16 values that enter P.V
+#pragma unroll
+      for (int e = 0; e < 8; ++e) l_run += pr[e];
+      pf[m] = __builtin_bit_cast(bf16x8_t, pk);
+    }
+    // 4. O^T += V^T P^T: A = V^T rows (dim 16 t + l % 16), keys 32m + 4 g4 .. +3 and 32m + 16 + 4 g4 .. +3
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const uint16_t* vr = &Vt[(16 * t + lane % 16) * VP + 4 * g4];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + 32 * m);
+        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 32 * m + 16);
+        const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pf[m], o[t], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // the tiles are rewritten next iteration
+  }
+
+  // row sums over the 4 lane groups of the query; lane l holds O^T dims 16 t + 4 g4 + r of query qi_lane
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  if (qi_lane >= lq) return;
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  uint16_t* op = g.out + int64_t(q0s + qi_lane) * g.o_st + int64_t(h) * g.o_sh + 4 * g4;
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    *reinterpret_cast<u32x2_t*>(op + 16 * t) =
+        u32x2_t{pack_bf16x2(o[t][0] * inv, o[t][1] * inv), pack_bf16x2(o[t][2] * inv, o[t][3] * inv)};
+  }
+}
+
+}  // namespace
+}  // namespace nvhip
+
+extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void* k, const void* v,
+                                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                            int64_t num_seqs, int64_t max_seqlen_q, int64_t Hq, int64_t Hkv,
+                                            int64_t D, int64_t q_stride_token, int64_t q_stride_head,
+                                            int64_t k_stride_token, int64_t v_stride_token,
+                                            int64_t out_stride_token, int64_t out_stride_head,
+                                            const int32_t* block_table, int64_t block_size, int64_t num_blocks,
+                                            int64_t max_blocks, float scale, int causal, void* stream) {
+  using namespace nvhip;
+  clear_error();
+  if (num_seqs < 0 || max_seqlen_q < 0 || Hq < 1 || Hkv < 1) return invalid("prefill_attention: bad size");
+  if (Hq % Hkv != 0) return invalid("prefill_attention: Hq must be a multiple of Hkv");
+  if (D != 64 && D != 128) return invalid("prefill_attention: head_dim must be 64 or 128");
+  if (q_stride_head < D || q_stride_token < Hq * q_stride_head || out_stride_head < D ||
+      out_stride_token < Hq * out_stride_head || q_stride_head % 8 || q_stride_token % 8 || out_stride_head % 4 ||
+      out_stride_token % 4)
+    return invalid("prefill_attention: bad q / out strides");
+  if (block_table == nullptr && (k_stride_token < Hkv * D || v_stride_token < Hkv * D || k_stride_token % 8 ||
+                                 v_stride_token % 8))
+    return invalid("prefill_attention: bad k / v strides");
+  if (block_table != nullptr && (block_size < 1 || num_blocks < 1 || max_blocks < 1))
+    return invalid("prefill_attention: bad block table shape");
+  if (num_seqs == 0 || max_seqlen_q == 0) return NVHIP_OK;
+  if (!out || !q || !k || !v || !cu_seqlens_q || !cu_seqlens_k) return invalid("prefill_attention: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || reinterpret_cast<uintptr_t>(out) % 8)
+    return invalid("prefill_attention: q, k, v must be 16-byte and out 8-byte aligned");
+  const int64_t qtiles = (max_seqlen_q + kBQ - 1) / kBQ;
+  if (qtiles > INT32_MAX || num_seqs > 65535 || Hq > 65535 || num_blocks > INT32_MAX ||
+      max_blocks * block_size > INT32_MAX)
+    return invalid("prefill_attention: size too large");
+  PrefillArgs g{static_cast<uint16_t*>(out),
+                static_cast<const uint16_t*>(q),
+                static_cast<const uint16_t*>(k),
+                static_cast<const uint16_t*>(v),
+                cu_seqlens_q,
+                cu_seqlens_k,
+                block_table,
+                q_stride_token,
+                q_stride_head,
+                block_table ? Hkv * D : k_stride_token,
+                block_table ? Hkv * D : v_stride_token,
+                out_stride_token,
+                out_stride_head,
+                int(Hkv),
+                int(Hq / Hkv),
+                int(block_size),
+                int(num_blocks),
+                int(max_blocks),
+                scale * 1.4426950408889634f,
+                causal ? 1 : 0};
+  const dim3 grid(static_cast<unsigned>(qtiles), static_cast<unsigned>(num_seqs), static_cast<unsigned>(Hq));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 64) hipLaunchKernelGGL(prefill_attention_kernel<64>, grid, dim3(kThreads), 0, s, g);
+  else hipLaunchKernelGGL(prefill_attention_kernel<128>, grid, dim3(kThreads), 0, s, g);
+  return check_launch("prefill_attention");
+}

@@ -11,8 +11,8 @@ eager), for each request that diverges the first divergent step and the torch ba
 candidates there (a near-tie flipped by a last-bit difference has a tiny gap), the graph replay time per decode step
 and the number of kernel nodes in each decode graph.
 
-The attention of the decode steps (shared by both backends) is the HIP paged decode attention by default
-(--attention torch: the harness's fp32 torch code). The hip backend's projections and LM head use the HIP GEMM by
+The attention (shared by both backends) is the HIP prefill and paged decode attention by default (--attention
+torch: the harness's fp32 torch code). The hip backend's projections and LM head use the HIP GEMM by
 default (--linear torch: torch's F.linear, as in the torch backend).
 
 Usage: python -m nanovllm_hip.harness.decode [--batch 32] [--steps 32] [--layers 28] [--min-len 512]
@@ -54,14 +54,15 @@ class Batch:
 
 
 @torch.inference_mode()
-def prefill(model, batch, backend, fp32_logits=False, reference=None, linear="hip"):
+def prefill(model, batch, backend, fp32_logits=False, reference=None, linear="hip", attention="hip"):
     """Prefills every request; returns its first generated token (greedy) and, where it differs from
     reference[i], this backend's logit gap between its token and the reference's."""
     first, gaps = [], {}
     for i, prompt in enumerate(batch.prompts):
         n = len(prompt)
         ctx = Context(True, batch.slots(i, range(n)).to(batch.device))
-        h = model.forward(prompt.to(batch.device), torch.arange(n, device=batch.device), ctx, backend, linear=linear)
+        h = model.forward(prompt.to(batch.device), torch.arange(n, device=batch.device), ctx, backend, attention,
+                          linear)
         logits = model.logits(h[-1:], fp32_logits, backend, linear)[0]
         tok = int(logits.argmax())
         if reference is not None and reference[i] != tok:
@@ -207,7 +208,7 @@ def main(argv=None):
 
     # hip backend: prefill, eager decode, graph decode from the same KV state
     cache = model.allocate_kv_cache(batch.num_blocks)
-    first_h, _ = prefill(model, batch, "hip", f32, linear=lin)
+    first_h, _ = prefill(model, batch, "hip", f32, linear=lin, attention=att)
     snapshot = cache.clone()
     tok_h, _, _ = decode(model, batch, first_h, args.steps, "hip", use_graph=False, fp32_logits=f32, attention=att,
                          linear=lin)
@@ -218,7 +219,7 @@ def main(argv=None):
     # torch backend (the reference): eager decode, compared step by step with the hip tokens (while a request's
     # history is identical its logits are directly comparable), then graph decode
     cache.zero_()
-    first_t, div_prefill = prefill(model, batch, "torch", f32, reference=first_h)
+    first_t, div_prefill = prefill(model, batch, "torch", f32, reference=first_h, attention=att)
     snapshot.copy_(cache)
     tok_t, div, _ = decode(model, batch, first_t, args.steps, "torch", use_graph=False, reference=tok_h,
                         fp32_logits=f32, attention=att)

@@ -23,7 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from nanovllm_hip import kernels as hip
-from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
+from nanovllm_hip.kernels.attention import flash_attn_varlen_func, flash_attn_with_kvcache
 
 
 @dataclass
@@ -207,7 +207,11 @@ class Qwen3:
                 cos, sin = self.cos_sin[positions].chunk(2, dim=-1)
                 q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
                 store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
-            if ctx.is_prefill:
+            if ctx.is_prefill and attention == "hip":
+                T = q.shape[0]
+                cu = torch.tensor([0, T], dtype=torch.int32, device=q.device)
+                o = flash_attn_varlen_func(q, k, v, T, cu, T, cu, self.scale, causal=True)
+            elif ctx.is_prefill:
                 o = prefill_attention(q, k, v, self.scale)
             elif attention == "hip":
                 B = ctx.context_lens.shape[0]

@@ -1,4 +1,10 @@
-"""Paged decode attention: the HIP replacement of the flash_attn_with_kvcache call in nano-vllm's decode path.
+"""Attention over the paged KV cache: the HIP replacements of the two flash-attn calls in nano-vllm's layers.
+
+flash_attn_varlen_func (prefill, nanovllm/layers/attention.py:77-83): variable-length causal attention over the
+new tokens' own k, v, or -- with a block table, the prefix cache -- over the paged caches. Kernel:
+csrc/prefill_attention.hip.
+
+flash_attn_with_kvcache (decode):
 
 nanovllm/layers/attention.py:84-90 reshapes q to [num_seqs, q_len, Hq, D] and calls
     flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=context_lens, block_table=block_tables,
@@ -36,3 +42,32 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
 
 
 paged_decode_attention = flash_attn_with_kvcache
+
+
+def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
+                           cu_seqlens_q: torch.Tensor, max_seqlen_k: int, cu_seqlens_k: torch.Tensor,
+                           softmax_scale: float | None = None, causal: bool = False,
+                           block_table: torch.Tensor | None = None) -> torch.Tensor:
+    """q [Tq, Hq, D] bf16 -> o [Tq, Hq, D]. Without block_table k, v are [Tk, Hkv, D] (the new tokens' own keys);
+    with it they are the paged caches [num_blocks, block_size, Hkv, D]. Query i of a sequence with lq queries and
+    lk keys sees keys j <= lk - lq + i when causal."""
+    assert q.dim() == 3 and q.dtype == torch.bfloat16 and q.stride(-1) == 1, (q.shape, q.dtype)
+    Tq, Hq, D = q.shape
+    assert k.dtype == v.dtype == torch.bfloat16 and k.shape == v.shape and k.shape[-1] == D
+    assert cu_seqlens_q.dtype == cu_seqlens_k.dtype == torch.int32 and cu_seqlens_q.shape == cu_seqlens_k.shape
+    if block_table is None:
+        assert k.dim() == 3 and k.stride(-1) == 1 and v.stride(-1) == 1
+        assert k.stride(1) == D and v.stride(1) == D, "heads of a k/v row must be contiguous"
+        Hkv = k.shape[1]
+    else:
+        assert k.dim() == 4 and k.is_contiguous() and v.is_contiguous()
+        assert block_table.dtype == torch.int32 and block_table.dim() == 2
+        assert block_table.shape[0] == cu_seqlens_q.shape[0] - 1
+        block_table = block_table.contiguous()
+        Hkv = k.shape[2]
+    assert Hq % Hkv == 0, (Hq, Hkv)
+    if q.stride(1) % 8 or q.stride(0) % 8:
+        q = q.contiguous()
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    return torch.ops.nvhip.prefill_attention(q, k, v, cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous(),
+                                             int(max_seqlen_q), scale, causal, block_table)

@@ -23,6 +23,8 @@ _DEF.define("fused_add_rms_norm_(Tensor x, Tensor(a!) residual, Tensor w, float 
 _DEF.define("silu_and_mul(Tensor x) -> Tensor")
 _DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
 _DEF.define("matmul_silu_mul(Tensor a, Tensor w) -> Tensor")
+_DEF.define("prefill_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
+            "int max_seqlen_q, float scale, bool causal, Tensor? block_table) -> Tensor")
 _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
             "Tensor slot_mapping) -> ()")
 _DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
@@ -227,3 +229,30 @@ _DEF.impl("matmul_silu_mul", _matmul_silu_mul_impl, "CUDA")
 @torch.library.register_fake("nvhip::matmul_silu_mul")
 def _matmul_silu_mul_fake(a, w):
     return torch.empty((a.shape[0], w.shape[0] // 2), dtype=a.dtype, device=a.device)
+
+
+# ------------------------------------------------------------------ prefill (varlen) attention
+
+def _prefill_attention_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, scale, causal, block_table):
+    Tq, Hq, D = q.shape
+    out = torch.empty((Tq, Hq, D), dtype=q.dtype, device=q.device)
+    if block_table is None:
+        Hkv, bt, bs, nb, mb = k.shape[1], None, 0, 0, 0
+        k_st, v_st = k.stride(0), v.stride(0)
+    else:
+        Hkv, bt, bs, nb, mb = k.shape[2], block_table.data_ptr(), k.shape[1], k.shape[0], block_table.shape[1]
+        k_st = v_st = Hkv * D
+    status = _lib.lib().nvhip_prefill_attention_bf16(
+        out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+        cu_seqlens_q.shape[0] - 1, max_seqlen_q, Hq, Hkv, D, q.stride(0), q.stride(1), k_st, v_st, out.stride(0),
+        out.stride(1), bt, bs, nb, mb, scale, int(causal), _lib.stream_of(q))
+    _lib.check(status, "prefill_attention")
+    return out
+
+
+_DEF.impl("prefill_attention", _prefill_attention_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::prefill_attention")
+def _prefill_attention_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, scale, causal, block_table):
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)

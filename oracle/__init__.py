@@ -19,6 +19,9 @@ Functions and the reference code each one follows (paths in R3pere/nano-vllm-tri
                      slot formula model_runner.py:340; flash-attn is not vendored in the reference (an unpinned
                      pyproject dependency), so its documented semantics (bottom-right causal mask, GQA head h -> kv
                      head h // (Hq / Hkv)) are restated and pinned by float64 SDPA, closed forms and invariants
+  varlen_attention   nanovllm/layers/attention.py:77-83 (flash_attn_varlen_func, prefill, with the prefix-cache block
+                     table of model_runner.py:311-312); pinned like the decode attention and by agreeing with it on
+                     one-query sequences
 
 How each is pinned (tests/test_oracle.py): closed forms in float64, hand-computed known answers, invariants
 (identity rotation, norm preservation, relative-position dependence, scale invariance), and brute-force loops on
@@ -29,6 +32,7 @@ from oracle.torch_ref import (  # noqa: F401
     apply_rotary_emb,
     matmul_fp64,
     paged_decode_attention,
+    varlen_attention,
     qk_norm_rope_kv,
     rms_forward,
     rope_cos_sin_cache,

@@ -129,3 +129,41 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         p = torch.nan_to_num(p, nan=0.0)                               # queries that see nothing
         out[b] = torch.einsum("hij,jhd->ihd", p, vb)
     return out.to(q.dtype)
+
+
+def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                     cu_seqlens_k: torch.Tensor, scale: float, causal: bool = True,
+                     block_table: torch.Tensor | None = None, compute_dtype=torch.float32) -> torch.Tensor:
+    """The prefill call of layers/attention.py:77-83, flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
+    max_seqlen_k, cu_seqlens_k, softmax_scale=scale, causal=True, block_table), restated.
+
+    q [Tq, Hq, D]; sequence b owns query rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1 and lk = cu_seqlens_k[b+1] -
+    cu_seqlens_k[b] keys: rows cu_seqlens_k[b] + j of k, v [Tk, Hkv, D], or with a block table (the prefix cache,
+    model_runner.py:311-312) slots block_table[b][j // bs] * bs + j % bs of the caches [blocks, bs, Hkv, D]. Query i
+    sees keys j <= lk - lq + i when causal (bottom-right alignment), all lk otherwise; head h reads kv head
+    h // (Hq / Hkv); a query that sees no key gets zeros. softmax(q.k * scale) @ v in compute_dtype."""
+    Tq, Hq, D = q.shape
+    out = torch.zeros(q.shape, dtype=compute_dtype)
+    for b in range(cu_seqlens_q.numel() - 1):
+        q0, q1 = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+        k0, k1 = int(cu_seqlens_k[b]), int(cu_seqlens_k[b + 1])
+        lq, lk = q1 - q0, k1 - k0
+        if lq <= 0 or lk <= 0:
+            continue
+        if block_table is None:
+            kb, vb = k[k0:k1], v[k0:k1]
+        else:
+            bs, hkv = k.shape[1], k.shape[2]
+            j = torch.arange(lk)
+            slots = block_table[b].long()[j // bs] * bs + j % bs
+            kb, vb = k.reshape(-1, hkv, D)[slots], v.reshape(-1, hkv, D)[slots]
+        g = Hq // kb.shape[1]
+        kb = kb.to(compute_dtype).repeat_interleave(g, dim=1)
+        vb = vb.to(compute_dtype).repeat_interleave(g, dim=1)
+        s = torch.einsum("ihd,jhd->hij", q[q0:q1].to(compute_dtype), kb) * scale
+        if causal:
+            limit = lk - lq + torch.arange(lq)
+            s = s.masked_fill(torch.arange(lk)[None, None, :] > limit[None, :, None], float("-inf"))
+        p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+        out[q0:q1] = torch.einsum("hij,jhd->ihd", p, vb)
+    return out.to(q.dtype)

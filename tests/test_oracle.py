@@ -384,3 +384,82 @@ def test_paged_attention_empty_context_is_zero():
     lens[1] = 0
     out = oracle.paged_decode_attention(q, kc, vc, lens, bt, 1.0, True, compute_dtype=torch.float64)
     assert torch.all(out[1] == 0)
+
+
+# ------------------------------------------------------------------ varlen (prefill) attention
+
+def _varlen_setup(lq=(5, 17, 1), lk=None, Hq=4, Hkv=2, D=16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    lk = lq if lk is None else lk
+    cq = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
+    ck = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
+    q = torch.randn(int(cq[-1]), Hq, D, generator=g, dtype=torch.float64)
+    k = torch.randn(int(ck[-1]), Hkv, D, generator=g, dtype=torch.float64)
+    v = torch.randn(int(ck[-1]), Hkv, D, generator=g, dtype=torch.float64)
+    return q, k, v, cq, ck
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("lq,lk", [((5, 17, 1), None), ((3, 4), (10, 4)), ((6,), (2,))])
+def test_varlen_attention_matches_sdpa_float64(lq, lk, causal):
+    """Per sequence against float64 scaled_dot_product_attention with an explicit bottom-right mask (prefix keys
+    when lk > lq; queries with no visible key give zeros, which SDPA leaves as NaN)."""
+    q, k, v, cq, ck = _varlen_setup(lq, lk)
+    out = oracle.varlen_attention(q, k, v, cq, ck, 0.25, causal, compute_dtype=torch.float64)
+    for b in range(len(lq)):
+        q0, q1, k0, k1 = int(cq[b]), int(cq[b + 1]), int(ck[b]), int(ck[b + 1])
+        nq, nk = q1 - q0, k1 - k0
+        mask = torch.ones(nq, nk, dtype=torch.bool)
+        if causal:
+            mask = torch.arange(nk)[None, :] <= (nk - nq + torch.arange(nq))[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            q[q0:q1].permute(1, 0, 2), k[k0:k1].repeat_interleave(2, dim=1).permute(1, 0, 2),
+            v[k0:k1].repeat_interleave(2, dim=1).permute(1, 0, 2), attn_mask=mask, scale=0.25).permute(1, 0, 2)
+        seen = mask.any(dim=1)
+        torch.testing.assert_close(out[q0:q1][seen], ref[seen], rtol=1e-12, atol=1e-12)
+        assert torch.all(out[q0:q1][~seen] == 0)
+
+
+def test_varlen_attention_causal_closed_forms():
+    """Equal keys: query i of a sequence with lq queries and lk keys returns the mean of the first lk - lq + i + 1
+    values; with lq == lk the first query returns exactly value 0."""
+    q, k, v, cq, ck = _varlen_setup((4, 7), (9, 7))
+    k[:] = 0.5
+    out = oracle.varlen_attention(q, k, v, cq, ck, 1.0, True, compute_dtype=torch.float64)
+    for b, (nq, nk) in enumerate([(4, 9), (7, 7)]):
+        for i in range(nq):
+            vis = nk - nq + i + 1
+            expect = v[int(ck[b]):int(ck[b]) + vis].mean(dim=0).repeat_interleave(2, dim=0)
+            torch.testing.assert_close(out[int(cq[b]) + i], expect, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(out[int(cq[1])], v[int(ck[1])].repeat_interleave(2, dim=0), rtol=0, atol=0)
+
+
+def test_varlen_with_block_table_equals_contiguous_and_decode():
+    """Keys read through a block table (the prefix cache) give the contiguous result; one query per sequence over
+    the paged cache is exactly the decode attention."""
+    q, k, v, cq, ck = _varlen_setup((3, 1, 5), (20, 9, 5), seed=4)
+    bs = 4
+    lk = [20, 9, 5]
+    nb = sum((n + bs - 1) // bs for n in lk) + 2
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1))
+    kc = torch.full((nb, bs, 2, 16), float("nan"), dtype=torch.float64)
+    vc = kc.clone()
+    bt = torch.full((3, 5), -1, dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(lk):
+        for c in range((n + bs - 1) // bs):
+            blk = int(perm[used]); used += 1
+            bt[b, c] = blk
+            rows = slice(int(ck[b]) + c * bs, int(ck[b]) + min(n, (c + 1) * bs))
+            cnt = rows.stop - rows.start
+            kc[blk, :cnt], vc[blk, :cnt] = k[rows], v[rows]
+    ref = oracle.varlen_attention(q, k, v, cq, ck, 0.3, True, compute_dtype=torch.float64)
+    paged = oracle.varlen_attention(q, kc, vc, cq, ck, 0.3, True, block_table=bt, compute_dtype=torch.float64)
+    torch.testing.assert_close(paged, ref, rtol=0, atol=0)
+    # one query per sequence == decode attention over the same cache
+    q1 = torch.stack([q[int(cq[b + 1]) - 1] for b in range(3)])          # the last query of each sequence
+    cq1 = torch.arange(4, dtype=torch.int32)
+    dec = oracle.paged_decode_attention(q1[:, None], kc, vc, torch.tensor(lk, dtype=torch.int32), bt, 0.3, True,
+                                        compute_dtype=torch.float64)[:, 0]
+    var = oracle.varlen_attention(q1, kc, vc, cq1, ck, 0.3, True, block_table=bt, compute_dtype=torch.float64)
+    torch.testing.assert_close(var, dec, rtol=0, atol=0)

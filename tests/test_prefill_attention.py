@@ -1,0 +1,134 @@
+"""GPU parity of the prefill (varlen) attention (nvhip_prefill_attention_bf16) against the oracle.
+
+The oracle restates flash_attn_varlen_func as nanovllm/layers/attention.py:77-83 calls it (fp32 from the same bf16
+inputs). The kernel rounds P to bf16 for P.V (as flash-attn does); tolerance: the bf16 output tolerance rtol 1.6e-2,
+atol 1e-2. Cases: a Qwen3-0.6B prefill batch (16 q / 8 kv heads, head_dim 128, k and v strided views of the qkv
+projection output), the prefix cache (keys through a block table of 256- and 16-slot blocks, NaN in unused slots),
+head_dim 64, GQA ratios 1 / 4 / 8, non-causal, more queries than keys (rows that see nothing are zero), an empty
+sequence, graph capture and replay.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from nanovllm_hip.kernels.attention import flash_attn_varlen_func
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def cu(lens):
+    return torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+
+
+def contiguous_case(lens, Hq=16, Hkv=8, D=128, seed=0, pad=64):
+    g = torch.Generator("cpu").manual_seed(seed)
+    T = sum(lens)
+    buf = torch.randn(T, (Hq + 2 * Hkv) * D + pad, generator=g).to(torch.bfloat16)
+    q = buf[:, :Hq * D].view(T, Hq, D)
+    k = buf[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
+    v = buf[:, (Hq + Hkv) * D:(Hq + 2 * Hkv) * D].view(T, Hkv, D)
+    return buf, q, k, v
+
+
+def check(q, k, v, cq, ck, causal=True, block_table=None, scale=None):
+    D = q.shape[-1]
+    scale = D ** -0.5 if scale is None else scale
+    lq = (cq[1:] - cq[:-1]).tolist()
+    lk = (ck[1:] - ck[:-1]).tolist()
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), max(lq), cq.to(DEV), max(lk), ck.to(DEV), scale,
+                                 causal, None if block_table is None else block_table.to(DEV))
+    ref = oracle.varlen_attention(q, k, v, cq, ck, scale, causal, block_table)
+    out = out.cpu()
+    assert out.shape == q.shape and torch.isfinite(out.float()).all()
+    torch.testing.assert_close(out.float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+    return out, ref
+
+
+def test_qwen3_prefill_batch_strided_views():
+    lens = [100, 300, 513, 1000]
+    buf, q, k, v = contiguous_case(lens, seed=1)
+    dbuf = buf.to(DEV)
+    T = sum(lens)
+    dq = dbuf[:, :2048].view(T, 16, 128)
+    dk = dbuf[:, 2048:3072].view(T, 8, 128)
+    dv = dbuf[:, 3072:4096].view(T, 8, 128)
+    cq = cu(lens)
+    out = flash_attn_varlen_func(dq, dk, dv, 1000, cq.to(DEV), 1000, cq.to(DEV), 128 ** -0.5, True)
+    ref = oracle.varlen_attention(q, k, v, cq, cq, 128 ** -0.5, True)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("lens", [[1], [63, 64, 65], [2, 129, 31, 250]])
+def test_lengths_around_tiles(lens):
+    _, q, k, v = contiguous_case(lens, seed=len(lens))
+    check(q.contiguous(), k.contiguous(), v.contiguous(), cu(lens), cu(lens))
+
+
+@pytest.mark.parametrize("block_size", [256, 16])
+def test_prefix_cache_block_table(block_size):
+    """lq new tokens attend over lk >= lq cached keys read through the block table (NaN in unused slots)."""
+    g = torch.Generator("cpu").manual_seed(block_size)
+    lq, lk = [37, 1, 200], [300, 70, 200]
+    Hq, Hkv, D = 16, 8, 128
+    nb = sum((n + block_size - 1) // block_size for n in lk) + 3
+    kc = torch.full((nb, block_size, Hkv, D), float("nan")).to(torch.bfloat16)
+    vc = kc.clone()
+    perm = torch.randperm(nb, generator=g)
+    maxb = max((n + block_size - 1) // block_size for n in lk)
+    bt = torch.full((3, maxb), -1, dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(lk):
+        for c in range((n + block_size - 1) // block_size):
+            blk = int(perm[used]); used += 1
+            bt[b, c] = blk
+            cnt = min(n - c * block_size, block_size)
+            kc[blk, :cnt] = torch.randn(cnt, Hkv, D, generator=g).to(torch.bfloat16)
+            vc[blk, :cnt] = torch.randn(cnt, Hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(sum(lq), Hq, D, generator=g).to(torch.bfloat16)
+    check(q, kc, vc, cu(lq), cu(lk), True, bt)
+
+
+def test_head_dim_64_and_gqa():
+    for Hq, Hkv, D in [(8, 8, 64), (16, 4, 128), (16, 2, 64)]:
+        _, q, k, v = contiguous_case([90, 200], Hq=Hq, Hkv=Hkv, D=D, seed=Hq + Hkv + D)
+        check(q.contiguous(), k.contiguous(), v.contiguous(), cu([90, 200]), cu([90, 200]))
+
+
+def test_non_causal_and_more_queries_than_keys():
+    _, q, k, v = contiguous_case([50, 120], seed=3)
+    check(q.contiguous(), k.contiguous(), v.contiguous(), cu([50, 120]), cu([50, 120]), causal=False)
+    g = torch.Generator("cpu").manual_seed(9)
+    q = torch.randn(40, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(10, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(10, 8, 128, generator=g).to(torch.bfloat16)
+    out, _ = check(q, k, v, cu([40]), cu([10]), causal=True)   # queries 0..29 see no key
+    assert torch.all(out[:30] == 0)
+
+
+def test_empty_sequence_in_the_batch():
+    _, q, k, v = contiguous_case([30, 0, 70], seed=5)
+    check(q.contiguous(), k.contiguous(), v.contiguous(), cu([30, 0, 70]), cu([30, 0, 70]))
+
+
+def test_graph_replay_matches_eager():
+    lens = [200, 333]
+    _, q, k, v = contiguous_case(lens, seed=6)
+    q, k, v = q.contiguous().to(DEV), k.contiguous().to(DEV), v.contiguous().to(DEV)
+    cq = cu(lens).to(DEV)
+    eager = flash_attn_varlen_func(q, k, v, 333, cq, 333, cq, 0.1, True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        flash_attn_varlen_func(q, k, v, 333, cq, 333, cq, 0.1, True)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = flash_attn_varlen_func(q, k, v, 333, cq, 333, cq, 0.1, True)
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
