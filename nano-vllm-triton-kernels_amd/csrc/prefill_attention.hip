@@ -8,8 +8,9 @@
 // paged caches [num_blocks, block_size, Hkv, D]. Query i of a sequence with lq queries sees keys j <= lk - lq + i
 // with causal (the mask aligned to the bottom right), all lk keys otherwise. Head h reads kv head h / (Hq / Hkv).
 //
-// One block (4 waves) per (64-query tile, sequence, q head); wave w owns queries 16w .. 16w+15 of the tile. Per
-// 64-key tile:
+// One block per (64-query tile, sequence, pair of q heads of one kv head -- or one head when Hq / Hkv is odd), 4
+// waves per head; wave w of a head owns queries 16w .. 16w+15 of the tile. The two heads share the K/V tiles (half
+// the K/V traffic of a block per head). Per 64-key tile:
 //   1. the K tile goes to LDS key-major ([64][D], 16-byte chunks, rows padded), the V tile dim-major ([D][64],
 //      transposed on the way in, so that a lane's keys of one dim are contiguous);
 //   2. S^T [16 keys x 16 queries] = K Q^T per 16-key subtile with v_mfma_f32_16x16x32_bf16 (K rows from LDS as the
@@ -48,19 +49,21 @@ struct PrefillArgs {
   int Hkv, G, bs, num_blocks, max_blocks;
   float scale_log2;
   int causal;
+  int qtiles, nhg;  // query tiles per sequence (from max_seqlen_q), head groups (Hq / heads per block)
 };
 
-// Element offset of key j of sequence b, kv head kvh, in k (v with v_st) -- or -1 if its cache block is invalid.
-template <int D>
-__device__ __forceinline__ int64_t key_row(const PrefillArgs& g, int b, int k0s, int j, int kvh, int64_t st) {
-  if (g.bt == nullptr) return int64_t(k0s + j) * st + int64_t(kvh) * D;
-  const int blk = g.bt[int64_t(b) * g.max_blocks + j / g.bs];
+// Element offset of key j of sequence b, kv head kvh, in k (v with v_st): a contiguous row, or (PAGED) the cache
+// slot of block blk (-1 if the block is not valid).
+template <int D, bool PAGED>
+__device__ __forceinline__ int64_t key_row(const PrefillArgs& g, int k0s, int j, int blk, int kvh, int64_t st) {
+  if constexpr (!PAGED) return int64_t(k0s + j) * st + int64_t(kvh) * D;
   if (blk < 0 || blk >= g.num_blocks) return -1;
   return ((int64_t(blk) * g.bs + j % g.bs) * g.Hkv + kvh) * D;
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const PrefillArgs g) {
+// HB q heads of one kv head per block (4 waves each, sharing the K/V tiles in LDS).
+template <int D, bool PAGED, int HB>
+__global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const PrefillArgs g) {
   constexpr int KC = D / 32;   // 32-wide dim steps of Q.K
   constexpr int DT = D / 16;   // 16-dim output tiles
   constexpr int CPR = D / 8;   // 16-byte chunks per K/V row
@@ -69,17 +72,26 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK * KP];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
 
-  const int qt = blockIdx.x, b = blockIdx.y, h = blockIdx.z, kvh = h / g.G;
+  // Block order: the ids are dealt round-robin over the 8 XCDs, so consecutive logical ids are taken 8 apart to
+  // keep all query tiles of one (sequence, head group) -- which read the same K/V -- on one XCD's L2; within a
+  // group the query tiles run from the last (the most keys) to the first.
+  int lid = blockIdx.x;
+  const int nblk = gridDim.x;
+  if (nblk % 8 == 0) lid = (lid % 8) * (nblk / 8) + lid / 8;
+  const int grp = lid / g.qtiles, qt = g.qtiles - 1 - lid % g.qtiles;
+  const int b = grp / g.nhg, hg = grp % g.nhg;
+  const int h = hg * HB + int(threadIdx.x) / kThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
   if (qt * kBQ >= lq || lk <= 0) {
-    if (qt * kBQ < lq && threadIdx.x < kBQ && qt * kBQ + int(threadIdx.x) < lq) {  // no keys: zero rows
-      uint16_t* o = g.out + int64_t(q0s + qt * kBQ + threadIdx.x) * g.o_st + int64_t(h) * g.o_sh;
+    const int r = int(threadIdx.x) % kThreads;
+    if (qt * kBQ < lq && r < kBQ && qt * kBQ + r < lq) {  // no keys: zero rows
+      uint16_t* o = g.out + int64_t(q0s + qt * kBQ + r) * g.o_st + int64_t(h) * g.o_sh;
       for (int d = 0; d < D; ++d) o[d] = 0;
     }
     return;
   }
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int tid = threadIdx.x, lane = tid % 64, wave = (tid % kThreads) / 64;
   const int qi_lane = qt * kBQ + 16 * wave + lane % 16;  // this lane's query (B operand row / O column)
   const int g4 = lane / 16;
 
@@ -101,30 +113,56 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   for (int t = 0; t < DT; ++t) o[t] = f32x4_t{0, 0, 0, 0};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  for (int kt0 = 0; kt0 < k_end; kt0 += kBK) {
-    // 1. K tile key-major: chunk c -> key c / CPR, dims (c % CPR) * 8; V tile: chunk c -> key c % 64, dims
-    // (c / 64) * 8, written transposed (lanes of a wave take consecutive keys of one dim chunk)
-    for (int c = tid; c < kBK * CPR; c += kThreads) {
-      const int key = c / CPR, dc = (c % CPR) * 8, j = kt0 + key;
-      u32x4 x = u32x4{0, 0, 0, 0};
-      if (j < lk) {
-        const int64_t row = key_row<D>(g, b, k0s, j, kvh, g.k_st);
-        if (row >= 0) x = *reinterpret_cast<const u32x4*>(g.k + row + dc);
-      }
-      *reinterpret_cast<u32x4*>(&Ks[key * KP + dc]) = x;
+  // 1. a tile's K and V chunks go global -> registers (all loads of a tile issued together; the next tile's loads
+  // are issued before this tile's MFMAs) -> LDS. K chunk c: key c / CPR, dims (c % CPR) * 8, stored key-major; V
+  // chunk c: key c % 64, dims (c / 64) * 8, stored transposed (a wave's lanes take consecutive keys of one dim
+  // chunk, so the 2-byte LDS writes of a lane group are contiguous). Invalid keys read the first 16 bytes of q and
+  // store zeros.
+  constexpr int NT = kThreads * HB;         // threads loading the tiles
+  constexpr int NL = kBK * CPR / NT;        // chunks per thread per operand
+  static_assert(NL >= 1 && NL * NT == kBK * CPR, "tile chunks per thread");
+  struct Regs {
+    u32x4 k[NL], v[NL];
+    uint32_t kok, vok;
+  };
+  const int32_t* bt_row = PAGED ? g.bt + int64_t(b) * g.max_blocks : nullptr;
+  auto gload = [&](Regs& R, int kt0) {
+    // block-table entries of this thread's keys first (PAGED), then every data load back to back
+    int kblk[NL], vblk = 0;
+    const int vj = kt0 + tid % kBK;  // V chunks of a thread share one key (NT is a multiple of kBK)
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int kj = kt0 + (tid + i * NT) / CPR;
+      kblk[i] = PAGED && kj < lk ? bt_row[kj / g.bs] : 0;
     }
-    for (int c = tid; c < kBK * CPR; c += kThreads) {
-      const int key = c % kBK, dc = (c / kBK) * 8, j = kt0 + key;
-      u32x4 x = u32x4{0, 0, 0, 0};
-      if (j < lk) {
-        const int64_t row = key_row<D>(g, b, k0s, j, kvh, g.v_st);
-        if (row >= 0) x = *reinterpret_cast<const u32x4*>(g.v + row + dc);
-      }
+    if constexpr (PAGED) vblk = vj < lk ? bt_row[vj / g.bs] : 0;
+    R.kok = R.vok = 0;
+    const int64_t vrow = vj < lk ? key_row<D, PAGED>(g, k0s, vj, vblk, kvh, g.v_st) : -1;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int c = tid + i * NT;
+      const int kj = kt0 + c / CPR;
+      const int64_t krow = kj < lk ? key_row<D, PAGED>(g, k0s, kj, kblk[i], kvh, g.k_st) : -1;
+      R.kok |= uint32_t(krow >= 0) << i;
+      R.vok |= uint32_t(vrow >= 0) << i;
+      R.k[i] = *reinterpret_cast<const u32x4*>(krow >= 0 ? g.k + krow + (c % CPR) * 8 : g.q);
+      R.v[i] = *reinterpret_cast<const u32x4*>(vrow >= 0 ? g.v + vrow + (c / kBK) * 8 : g.q);
+    }
+  };
+  auto lstore = [&](const Regs& R) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int c = tid + i * NT;
+      const u32x4 zero = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Ks[(c / CPR) * KP + (c % CPR) * 8]) = ((R.kok >> i) & 1) ? R.k[i] : zero;
+      const u32x4 x = ((R.vok >> i) & 1) ? R.v[i] : zero;
+      const int key = c % kBK, dc = (c / kBK) * 8;
 #pragma unroll
       for (int e = 0; e < 8; ++e) Vt[(dc + e) * VP + key] = uint16_t(x[e / 2] >> (16 * (e & 1)));
     }
-    __syncthreads();
+  };
 
+  auto tile = [&](int kt0) {
     // 2. S^T per 16-key subtile: lane holds keys kt0 + 16 st + 4 g4 + r of query qi_lane
     f32x4_t s[4];
 #pragma unroll
@@ -185,7 +223,21 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
         o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pf[m], o[t], 0, 0, 0);
       }
     }
-    __syncthreads();  // the tiles are rewritten next iteration
+  };
+  // The next tile's loads are issued into the register set right after it has been stored to LDS, so they are in
+  // flight while this tile is computed (past the last tile the last one is loaded again, unused; every load is
+  // issued unconditionally so the compiler's waits are exact). Two tiles ahead measured no faster.
+  if (k_end > 0) {
+    const int last = (k_end - 1) / kBK * kBK;
+    Regs A;
+    gload(A, 0);
+    for (int kt0 = 0; kt0 < k_end; kt0 += kBK) {
+      lstore(A);
+      __syncthreads();
+      gload(A, min(kt0 + kBK, last));
+      tile(kt0);
+      __syncthreads();  // the LDS tiles are rewritten next
+    }
   }
 
   // row sums over the 4 lane groups of the query; lane l holds O^T dims 16 t + 4 g4 + r of query qi_lane
@@ -231,7 +283,7 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || reinterpret_cast<uintptr_t>(out) % 8)
     return invalid("prefill_attention: q, k, v must be 16-byte and out 8-byte aligned");
   const int64_t qtiles = (max_seqlen_q + kBQ - 1) / kBQ;
-  if (qtiles > INT32_MAX || num_seqs > 65535 || Hq > 65535 || num_blocks > INT32_MAX ||
+  if (qtiles > INT32_MAX || num_seqs > INT32_MAX || num_blocks > INT32_MAX ||
       max_blocks * block_size > INT32_MAX)
     return invalid("prefill_attention: size too large");
   PrefillArgs g{static_cast<uint16_t*>(out),
@@ -253,10 +305,26 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
                 int(num_blocks),
                 int(max_blocks),
                 scale * 1.4426950408889634f,
-                causal ? 1 : 0};
-  const dim3 grid(static_cast<unsigned>(qtiles), static_cast<unsigned>(num_seqs), static_cast<unsigned>(Hq));
+                causal ? 1 : 0,
+                0,
+                0};
+  const int hb = (Hq / Hkv) % 2 == 0 ? 2 : 1;  // q heads per block
+  g.qtiles = int(qtiles);
+  g.nhg = int(Hq / hb);
+  const int64_t blocks = qtiles * num_seqs * (Hq / hb);
+  if (blocks > INT32_MAX) return invalid("prefill_attention: size too large");
+  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kThreads * hb));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 64) hipLaunchKernelGGL(prefill_attention_kernel<64>, grid, dim3(kThreads), 0, s, g);
-  else hipLaunchKernelGGL(prefill_attention_kernel<128>, grid, dim3(kThreads), 0, s, g);
+  const bool paged = block_table != nullptr;
+#define NVHIP_PREFILL_LAUNCH(DD, PG, HBV) hipLaunchKernelGGL((prefill_attention_kernel<DD, PG, HBV>), grid, block, 0, s, g)
+  if (hb == 2 && D == 64 && paged) NVHIP_PREFILL_LAUNCH(64, true, 2);
+  else if (hb == 2 && D == 64) NVHIP_PREFILL_LAUNCH(64, false, 2);
+  else if (hb == 2 && paged) NVHIP_PREFILL_LAUNCH(128, true, 2);
+  else if (hb == 2) NVHIP_PREFILL_LAUNCH(128, false, 2);
+  else if (D == 64 && paged) NVHIP_PREFILL_LAUNCH(64, true, 1);
+  else if (D == 64) NVHIP_PREFILL_LAUNCH(64, false, 1);
+  else if (paged) NVHIP_PREFILL_LAUNCH(128, true, 1);
+  else NVHIP_PREFILL_LAUNCH(128, false, 1);
+#undef NVHIP_PREFILL_LAUNCH
   return check_launch("prefill_attention");
 }
