@@ -88,3 +88,48 @@ def test_check_maps_status_to_exceptions():
     with pytest.raises(_lib.KernelError):
         _lib.check(_lib.NVHIP_ELAUNCH, "silu")
     _lib.check(_lib.NVHIP_OK, "silu")
+
+
+def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching():
+    lib = _lib.lib()
+    P = None
+    dec = lib.nvhip_paged_decode_attention_bf16
+
+    def decode(num_seqs=2, q_len=1, Hq=16, Hkv=8, D=128, bs=256, nb=4, mb=2, qst=2048, qsh=128, ost=2048, osh=128):
+        return dec(P, P, P, P, P, P, num_seqs, q_len, Hq, Hkv, D, bs, nb, mb, qst, qsh, ost, osh, 0.1, 1, P, 0, P)
+
+    assert decode(Hq=12) == _lib.NVHIP_EINVAL and "multiple" in _err()
+    assert decode(D=96) == _lib.NVHIP_EINVAL and "head_dim" in _err()
+    assert decode(q_len=3, Hq=16, Hkv=2) == _lib.NVHIP_EINVAL and "<= 16" in _err()   # 24 rows per kv head
+    assert decode(qsh=100) == _lib.NVHIP_EINVAL and "strides" in _err()
+    assert decode(num_seqs=0) == _lib.NVHIP_OK
+    assert decode() == _lib.NVHIP_EINVAL and "null" in _err()
+    ws = lib.nvhip_paged_decode_attention_workspace_size
+    assert ws(32, 1, 16, 8, 128, 256, 8) == 0                 # 256 (sequence, kv head) pairs: no split
+    assert ws(1, 1, 16, 8, 128, 256, 64) > 0                  # one long sequence: split over blocks
+    assert ws(1, 1, 16, 8, 128, 256, 64) == 8 * 32 * 2 * (2 + 128) * 4   # 8 pairs x 32 splits of 512 tokens, 2 rows
+    assert ws(0, 1, 16, 8, 128, 256, 8) == 0
+
+    pre = lib.nvhip_prefill_attention_bf16
+
+    def prefill(num_seqs=2, maxq=64, Hq=16, Hkv=8, D=128, kst=4160, bt=None, bs=0, nb=0, mb=0):
+        return pre(P, P, P, P, P, P, num_seqs, maxq, Hq, Hkv, D, 4160, 128, kst, kst, 2048, 128, bt, bs, nb, mb,
+                   0.1, 1, P)
+
+    assert prefill(D=256) == _lib.NVHIP_EINVAL and "head_dim" in _err()
+    assert prefill(kst=1000) == _lib.NVHIP_EINVAL and "k / v strides" in _err()
+    assert prefill(bt=ctypes.c_void_p(64), bs=0) == _lib.NVHIP_EINVAL and "block table" in _err()
+    assert prefill(maxq=0) == _lib.NVHIP_OK
+    assert prefill() == _lib.NVHIP_EINVAL and "null" in _err()
+
+    st = lib.nvhip_store_kvcache
+    assert st(P, P, P, P, 1024, 1024, P, 64, 4, 1024, 3, P) == _lib.NVHIP_EINVAL and "element size" in _err()
+    assert st(P, P, P, P, 512, 1024, P, 64, 4, 1024, 2, P) == _lib.NVHIP_EINVAL and "stride" in _err()
+    assert st(P, P, P, P, 1024, 1024, P, 64, 0, 1024, 2, P) == _lib.NVHIP_OK
+    assert st(P, P, P, P, 1024, 1024, P, 64, 4, 1024, 2, P) == _lib.NVHIP_EINVAL and "null" in _err()
+
+    fm = lib.nvhip_matmul_silu_mul_bf16
+    assert fm(P, P, P, 4, 8, 12, 16, 16, 8, P) == _lib.NVHIP_EINVAL and "null" in _err()
+    assert fm(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 4, 8, 12, 16, 16, 8, P) == \
+        _lib.NVHIP_EINVAL and "K % 8" in _err()
+    assert fm(P, P, P, 0, 8, 16, 16, 16, 8, P) == _lib.NVHIP_OK
