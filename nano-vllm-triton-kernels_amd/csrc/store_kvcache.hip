@@ -7,7 +7,7 @@
 // contiguous: blocks x block_size slots). Slots outside [0, num_slots) -- the padding value -1 -- are skipped.
 //
 // One thread per 16-byte chunk of a row, flattened over (token, chunk) with a grid-stride loop; the slot is read
-// by every thread of its token (cached). Rows whose base or stride is not 16-byte aligned go through a 2/4-byte
+// by every thread of its token (cached), alongside the row loads. Rows whose base or stride is not 16-byte aligned go through a 2/4-byte
 // element loop instead. The data is copied as raw bits (bf16, fp16 or fp32).
 #include <algorithm>
 
@@ -30,12 +30,14 @@ __global__ __launch_bounds__(256) void store_kvcache_vec(const StoreArgs g) {
   const int64_t chunks = g.row_bytes / 16, total = g.n * chunks;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
     const int64_t t = i / chunks, c = (i - t * chunks) * 16;
+    // the row loads do not wait for the slot (a padded token's row is read and dropped); the rows are written
+    // with the nontemporal hint, as the fused kernel writes its cache rows
     const int32_t slot = g.slots[t];
-    if (slot < 0 || slot >= g.num_slots) continue;
     const u32x4 kv = *reinterpret_cast<const u32x4*>(g.k + t * g.k_stride + c);
     const u32x4 vv = *reinterpret_cast<const u32x4*>(g.v + t * g.v_stride + c);
-    *reinterpret_cast<u32x4*>(g.kc + int64_t(slot) * g.row_bytes + c) = kv;
-    *reinterpret_cast<u32x4*>(g.vc + int64_t(slot) * g.row_bytes + c) = vv;
+    if (slot < 0 || slot >= g.num_slots) continue;
+    __builtin_nontemporal_store(kv, reinterpret_cast<u32x4*>(g.kc + int64_t(slot) * g.row_bytes + c));
+    __builtin_nontemporal_store(vv, reinterpret_cast<u32x4*>(g.vc + int64_t(slot) * g.row_bytes + c));
   }
 }
 
