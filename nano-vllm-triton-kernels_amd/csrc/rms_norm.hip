@@ -47,9 +47,12 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const NormArgs a) {
   }
 
   float v[VPL][8];
-  u32x4 raw[VPL];
+  u32x4 raw[VPL], wraw[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) raw[j] = load8<true>(xr + (j * LANES + sub) * 8);
+  // the weight is loaded up front: after the residual store the compiler could not move it past a possible alias
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) wraw[j] = load8<true>(a.w + (j * LANES + sub) * 8);
   if constexpr (ADD) {
     u32x4 rraw[VPL];
 #pragma unroll
@@ -79,10 +82,14 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const NormArgs a) {
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     float wf[8], o[8];
-    unpack8(load8<true>(a.w + (j * LANES + sub) * 8), wf);
+    unpack8(wraw[j], wf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = round_bf16(v[j][i] * rstd) * wf[i];
-    store8<true>(a.y + row * N + (j * LANES + sub) * 8, pack8(o));
+    uint16_t* dst = a.y + row * N + (j * LANES + sub) * 8;
+    // plain RMSNorm streams its output (measured faster); Add+RMSNorm keeps plain stores (measured slower with the
+    // hint on either output)
+    if constexpr (ADD) store8<true>(dst, pack8(o));
+    else __builtin_nontemporal_store(pack8(o), reinterpret_cast<u32x4*>(dst));
   }
 }
 
