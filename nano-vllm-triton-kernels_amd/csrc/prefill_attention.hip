@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
     }
     return;
   }
-  const int tid = threadIdx.x, lane = tid % 64, wave = (tid % kThreads) / 64;
+  const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane((tid % kThreads) / 64);
   const int qi_lane = qt * kBQ + 16 * wave + lane % 16;  // this lane's query (B operand row / O column)
   const int g4 = lane / 16;
 
@@ -107,6 +107,7 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
   const int q_last = min(qt * kBQ + kBQ, lq) - 1;
   const int k_end = g.causal ? min(lk, diag + q_last + 1) : lk;  // keys this block needs
   const int limit_lane = g.causal ? diag + qi_lane : lk - 1;      // last key of this lane's query
+  const int wave_q0 = qt * kBQ + 16 * wave;                        // the wave's first query
 
   f32x4_t o[DT];
 #pragma unroll
@@ -174,14 +175,17 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
         s[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(kr + 32 * c), qf[c], s[st],
                                                         0, 0, 0);
     }
-    // 3. online softmax of query qi_lane over this tile
+    // 3. online softmax of query qi_lane over this tile. Only a tile that reaches past the key count or past the
+    // causal limit of the wave's first query needs the mask (wave-uniform test). 2^x is the hardware v_exp_f32:
+    // its arguments are <= 0 here and only results below the fp32 normal range (which flush to 0) differ from exp2f.
+    const bool full = kt0 + kBK <= lk && (!g.causal || kt0 + kBK - 1 <= diag + wave_q0);
     float tmax = -INFINITY;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = kt0 + 16 * st + 4 * g4 + r;
-        const float v = (j < lk && j <= limit_lane) ? s[st][r] * g.scale_log2 : -INFINITY;
+        const float v = (full || (j < lk && j <= limit_lane)) ? s[st][r] * g.scale_log2 : -INFINITY;
         s[st][r] = v;
         tmax = fmaxf(tmax, v);
       }
@@ -189,11 +193,13 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    m_run = m_new;
-    l_run *= alpha;
+    if (__ballot(m_new != m_run) != 0) {  // some row's max moved: rescale (most later tiles skip this)
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      l_run *= alpha;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+      for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    }
+    m_run = m_new;
     // p as bf16, packed per 32-key step in the k-slot order of the P.V product
     bf16x8_t pf[2];
 #pragma unroll
@@ -201,8 +207,8 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
       float p[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[r] = exp2f(s[2 * m][r] - m_use);
-        p[4 + r] = exp2f(s[2 * m + 1][r] - m_use);
+        p[r] = __builtin_amdgcn_exp2f(s[2 * m][r] - m_use);
+        p[4 + r] = __builtin_amdgcn_exp2f(s[2 * m + 1][r] - m_use);
       }
       const u32x4 pk = pack8(p);
       float pr[8];
