@@ -16,11 +16,12 @@ T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNo
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
 the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s; the causal
-prefill attention of one layer over 4 sequences of 2048 tokens, in TFLOP/s.
+prefill attention of one layer over 4 sequences of 2048 tokens, in TFLOP/s; the end-to-end decode step of a
+random-init Qwen3-0.6B-shaped model (batch 32, HIP graph: us per step, tokens/s, kernel nodes).
 The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
 sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 8192] [--no-cpu] [--no-extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 8192] [--no-cpu] [--no-extra] [--no-e2e]
 """
 import argparse
 import json
@@ -270,6 +271,32 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048):
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
+def e2e_decode_step(torch, dev, batch=32, layers=28, min_len=512, max_len=2048, reps=20):
+    """One decode step of a random-init Qwen3-0.6B-shaped model (28 layers, tied embeddings, bf16) for 32 sequences
+    with prompts of U[512, 2048] random ids in 256-slot paged blocks, through the hip backend (the HIP kernels for
+    the norms, the fused pre-attention kernel, every projection and the LM head, gate_up with the SiLU epilogue, the
+    paged decode attention), replayed from a HIP graph: microseconds per step, tokens per second, kernel nodes.
+    The prompts are prefilled first (HIP prefill attention) so the caches hold real K/V."""
+    from nanovllm_hip.harness.decode import Batch, DecodeStep, graph_nodes, prefill, replay_us
+    from nanovllm_hip.harness.qwen3 import Qwen3, Qwen3Config
+    cfg = Qwen3Config(num_hidden_layers=layers)
+    model = Qwen3(cfg, dev, seed=0)
+    b = Batch(cfg, batch, 4, min_len, max_len, 0, dev)
+    model.allocate_kv_cache(b.num_blocks)
+    first, _ = prefill(model, b, "hip")
+    step = DecodeStep(model, b, "hip")
+    with torch.inference_mode():
+        step.set_inputs(first, 0)
+        step.capture()
+    us = replay_us(step, reps)
+    kernels_n, nodes = graph_nodes(step.graph)
+    out = {"us": round(us, 1), "tokens_per_s": round(batch / (us * 1e-6), 1), "kernels": kernels_n,
+           "context_tokens": sum(b.lens), "batch": batch, "layers": layers}
+    del step, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_ceiling(torch, dev, mib=1024, reps=20):
     """Device copy (torch copy_) of `mib` MiB: the practical read+write bandwidth ceiling, in GB/s."""
     n = mib * 2 ** 20 // 2
@@ -325,6 +352,7 @@ def main():
     p.add_argument("--tokens", type=int, default=8192)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="only the headline kernel")
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode step (part of the extras)")
     p.add_argument("--profile-gemm", action="store_true",
                    help="for rocprofv3 runs: --steps eager launches of the bf16 GEMM at each Qwen3-0.6B projection "
                         "shape (M = --gemm-m), each followed by torch.nn.functional.linear on the same tensors")
@@ -374,6 +402,8 @@ def main():
     if not args.no_extra:
         result["extra"] = extras(torch, oracle, kernels, dev, args.steps)
         result["extra"]["copy_ceiling_GB/s"] = copy_ceiling(torch, dev)
+        if not args.no_e2e:
+            result["extra"]["e2e_decode_step"] = e2e_decode_step(torch, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, oracle, T)
     print(json.dumps(result), flush=True)
