@@ -271,7 +271,7 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048):
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
-def e2e_decode_step(torch, dev, batch=32, layers=28, min_len=512, max_len=2048, reps=20):
+def e2e_decode_step(torch, dev, batch=32, layers=28, min_len=512, max_len=2048, reps=20, profile_replays=0):
     """One decode step of a random-init Qwen3-0.6B-shaped model (28 layers, tied embeddings, bf16) for 32 sequences
     with prompts of U[512, 2048] random ids in 256-slot paged blocks, through the hip backend (the HIP kernels for
     the norms, the fused pre-attention kernel, every projection and the LM head, gate_up with the SiLU epilogue, the
@@ -288,6 +288,12 @@ def e2e_decode_step(torch, dev, batch=32, layers=28, min_len=512, max_len=2048, 
     with torch.inference_mode():
         step.set_inputs(first, 0)
         step.capture()
+    if profile_replays:  # for a rocprofv3 kernel trace: eager-synchronised replays, nothing else launched
+        torch.cuda.synchronize()
+        for _ in range(profile_replays):
+            step.graph.replay()
+        torch.cuda.synchronize()
+        print(f"profile: {profile_replays} decode-step graph replays", flush=True)
     us = replay_us(step, reps)
     kernels_n, nodes = graph_nodes(step.graph)
     out = {"us": round(us, 1), "tokens_per_s": round(batch / (us * 1e-6), 1), "kernels": kernels_n,
@@ -357,6 +363,9 @@ def main():
                    help="for rocprofv3 runs: --steps eager launches of the bf16 GEMM at each Qwen3-0.6B projection "
                         "shape (M = --gemm-m), each followed by torch.nn.functional.linear on the same tensors")
     p.add_argument("--gemm-m", type=int, default=2048, help="M of the --profile-gemm products")
+    p.add_argument("--profile-e2e", action="store_true",
+                   help="for rocprofv3 kernel traces: build the Qwen3-0.6B-shaped model, prefill, capture the batch-32 "
+                        "decode step and replay it --steps times, then print the e2e line")
     p.add_argument("--profile", action="store_true",
                    help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
                         "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
@@ -375,6 +384,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.profile_gemm:
         profile_gemm(torch, kernels, dev, args.steps, args.gemm_m)
+        return
+    if args.profile_e2e:
+        print(json.dumps(e2e_decode_step(torch, dev, profile_replays=args.steps)), flush=True)
         return
     T = args.tokens
     wl = FusedWorkload(T, dev, torch, oracle)
