@@ -41,6 +41,7 @@ HQ, HKV, D, MAX_POS, THETA, BLOCK, EPS = 16, 8, 128, 40960, 1e6, 256, 1e-6
 NUM_BLOCKS = 512
 PAD = 64
 NSETS = 4
+WARM_S = 0.05  # minimum warm-up wall time of every extra measurement (clock ramp)
 GEMM_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}  # (K, N)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qk_norm_rope_kv_t8192_traffic.json")
 
@@ -92,9 +93,14 @@ class FusedWorkload:
                                self.k_cache, self.v_cache, s["slots"], False)
 
 
-def time_graph(torch, fn, n_calls, steps, warmup):
+def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
     """Records n_calls calls of fn(i) into one HIP graph, replays it (warmup + steps calls, rounded up to whole
-    replays) and returns the average milliseconds per call, timed with events on the replay stream."""
+    replays) and returns the average milliseconds per call, timed with events on the replay stream.
+
+    min_warm_s: keep warming up until that much wall time has passed. The GPU raises its clocks over several
+    milliseconds of load, and a measurement that starts right after host-side set-up (where the GPU idled) reads
+    10-20 % slow for a compute-bound kernel; the extras use 50 ms so that every kernel and its torch comparison
+    start from the same state."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -108,8 +114,16 @@ def time_graph(torch, fn, n_calls, steps, warmup):
             fn(i)
     reps_warm = max(1, -(-warmup // n_calls))
     reps = max(1, -(-steps // n_calls))
+    t0 = time.perf_counter()
     for _ in range(reps_warm):
         graph.replay()
+    torch.cuda.synchronize()
+    batch = reps_warm
+    while time.perf_counter() - t0 < min_warm_s:
+        for _ in range(batch):
+            graph.replay()
+        torch.cuda.synchronize()
+        batch *= 2
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -155,13 +169,13 @@ def extras(torch, oracle, kernels, dev, steps):
     out = {}
     for T in (1, 32, 2048):
         wl = FusedWorkload(T, dev, torch, oracle, seed=T)
-        ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, max(40, steps), 20)
+        ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, max(40, steps), 20, WARM_S)
         out[f"qk_norm_rope_kv_T{T}"] = {"us": round(ms * 1e3, 3),
                                         "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1)}
     wl = FusedWorkload(8192, dev, torch, oracle, seed=5)
     ms, _ = time_graph(torch, lambda i: kernels.store_kvcache(wl.sets[i % NSETS]["k"], wl.sets[i % NSETS]["v"],
                                                               wl.k_cache, wl.v_cache, wl.sets[i % NSETS]["slots"]),
-                       NSETS, max(40, steps), 20)
+                       NSETS, max(40, steps), 20, WARM_S)
     nbytes = 8192 * (4 * HKV * D * 2 + 4)
     gbs = nbytes / (ms * 1e-3) / 1e9
     out["store_kvcache_T8192"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
@@ -177,7 +191,7 @@ def extras(torch, oracle, kernels, dev, steps):
             ("fused_add_rms_norm_T8192", lambda i: kernels.fused_add_rms_norm(xs[i], rs[i], w, EPS),
              (4 * T * H + H) * 2),
             ("silu_and_mul_T8192", lambda i: kernels.silu_and_mul(gus[i]), 3 * T * I * 2)):
-        ms, _ = time_graph(torch, fn, NSETS, max(40, steps), 20)
+        ms, _ = time_graph(torch, fn, NSETS, max(40, steps), 20, WARM_S)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     del xs, rs, gus
@@ -186,9 +200,9 @@ def extras(torch, oracle, kernels, dev, steps):
         a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
         wt = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
         b = wt.t()
-        ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 4, max(40, steps), 20)
+        ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 4, max(40, steps), 20, WARM_S)
         tf = 2 * M * N * K / (ms * 1e-3) / 1e12
-        ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, wt), 4, max(40, steps), 20)
+        ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, wt), 4, max(40, steps), 20, WARM_S)
         out[f"gemm_bf16_{layer}_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
                                            "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
                                            "torch_linear_us": round(ms_ref * 1e3, 2)}
@@ -201,8 +215,8 @@ def extras(torch, oracle, kernels, dev, steps):
         a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
         w0 = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
         ws = [w0.clone() for _ in range(nw)]
-        ms, _ = time_graph(torch, lambda i: kernels.matmul(a, ws[i].t()), nw, max(nw, steps), nw)
-        ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, ws[i]), nw, max(nw, steps), nw)
+        ms, _ = time_graph(torch, lambda i: kernels.matmul(a, ws[i].t()), nw, max(nw, steps), nw, WARM_S)
+        ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, ws[i]), nw, max(nw, steps), nw, WARM_S)
         nbytes = 2 * (M * K + N * K + M * N)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"gemm_bf16_{layer}_M{M}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -214,8 +228,8 @@ def extras(torch, oracle, kernels, dev, steps):
     n = 4096
     a = torch.randn(n, n, generator=g).to(dev)
     b = torch.randn(n, n, generator=g).to(dev)
-    ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 1, 5, 2)
-    ms_ref, _ = time_graph(torch, lambda i: torch.matmul(a, b), 1, 5, 2)
+    ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 1, 5, 2, WARM_S)
+    ms_ref, _ = time_graph(torch, lambda i: torch.matmul(a, b), 1, 5, 2, WARM_S)
     tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
     out["gemm_fp32_ieee_4096"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
                                   "frac_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4),
@@ -245,7 +259,7 @@ def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
         sets.append((q, kc, vc, lens.to(torch.int32).to(dev), bt.to(dev)))
     scale = D ** -0.5
     ms, _ = time_graph(torch, lambda i: flash_attn_with_kvcache(*sets[i % NSETS], scale, True), NSETS,
-                       max(40, steps), 8)
+                       max(40, steps), 8, WARM_S)
     ctx = int(lens.sum())
     nbytes = ctx * HKV * D * 2 * 2 + 2 * batch * HQ * D * 2 + batch * 4 + sum(need) * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -265,7 +279,7 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048):
     v = buf[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].view(T, HKV, D)
     cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=dev)
     ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True), 4,
-                       max(20, steps // 4), 4)
+                       max(20, steps // 4), 4, WARM_S)
     flops = 4 * D * HQ * nseq * L * (L + 1) // 2
     tf = flops / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
@@ -308,7 +322,7 @@ def copy_ceiling(torch, dev, mib=1024, reps=20):
     n = mib * 2 ** 20 // 2
     src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
     dst = torch.empty_like(src)
-    for _ in range(3):
+    for _ in range(20):
         dst.copy_(src)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -354,7 +368,7 @@ def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--tokens", type=int, default=8192)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="only the headline kernel")

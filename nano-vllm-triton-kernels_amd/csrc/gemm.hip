@@ -545,16 +545,30 @@ int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   return check_launch("matmul");
 }
 
-// Tile shape by output size (measured on MI355X at the Qwen3-0.6B projections, M = 2048): the largest tile that
-// still gives >= 192 tiles (3/4 of the 256 CUs); 64x64 tiles for 32 < M <= 64.
+// Tile shape by a cost model fitted on MI355X at the Qwen3-0.6B projections: a launch runs in ceil(tiles / 256)
+// rounds of one tile per CU, so its time goes as rounds x tile area / efficiency, the efficiency of a tile growing
+// with its size (fewer L2 bytes per flop). At M = 2048 this picks 128x256 for N = 4096, 256x192 for N = 6144 and
+// 64x128 for N = 1024 -- 256 tiles each, the fastest of a sweep over eleven shapes. 64x64 tiles for 32 < M <= 64.
 template <int RS, bool KTAIL, bool SILU>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
-  auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
   if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU>(g, s);
-  if (tiles(256, 256) >= 192) return launch_mfma<256, 256, 4, 2, 1, KTAIL, SILU>(g, s);
-  if (tiles(128, 256) >= 192) return launch_mfma<128, 256, 2, 2, RS, KTAIL, SILU>(g, s);
-  if (tiles(128, 128) >= 192) return launch_mfma<128, 128, 2, 4, RS, KTAIL, SILU>(g, s);
-  return launch_mfma<128, 64, 2, 2, RS, KTAIL, SILU>(g, s);
+  struct Shape { int bm, bn; double eff; };
+  constexpr Shape shapes[] = {{256, 256, 1.0}, {256, 192, 1.0}, {128, 256, 0.95}, {128, 128, 0.85}, {64, 128, 0.75}};
+  constexpr int kCUs = 256;
+  int best = 0;
+  double best_cost = 0.0;
+  for (int i = 0; i < 5; ++i) {
+    const int64_t tiles = int64_t((g.M + shapes[i].bm - 1) / shapes[i].bm) * ((g.N + shapes[i].bn - 1) / shapes[i].bn);
+    const double cost = double((tiles + kCUs - 1) / kCUs) * shapes[i].bm * shapes[i].bn / shapes[i].eff;
+    if (i == 0 || cost < best_cost) best = i, best_cost = cost;
+  }
+  switch (best) {
+    case 0: return launch_mfma<256, 256, 4, 2, 1, KTAIL, SILU>(g, s);
+    case 1: return launch_mfma<256, 192, 4, 2, RS, KTAIL, SILU>(g, s);
+    case 2: return launch_mfma<128, 256, 2, 2, RS, KTAIL, SILU>(g, s);
+    case 3: return launch_mfma<128, 128, 2, 4, RS, KTAIL, SILU>(g, s);
+    default: return launch_mfma<64, 128, 2, 2, RS, KTAIL, SILU>(g, s);
+  }
 }
 
 // 8 waves per block; 4 k steps of loads per wave in flight for wide outputs, 8 when N < 2048 (fewer blocks, each

@@ -161,9 +161,12 @@ def graph_nodes(graph):
     return kernels, n.value
 
 
-def replay_us(step, reps):
+def replay_us(step, reps, warm=10):
+    """Average microseconds per replay of the captured step, after `warm` untimed replays (the GPU raises its
+    clocks over the first milliseconds of load)."""
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    step.graph.replay()
+    for _ in range(warm):
+        step.graph.replay()
     torch.cuda.synchronize()
     start.record()
     for _ in range(reps):
