@@ -8,20 +8,25 @@
 // paged caches [num_blocks, block_size, Hkv, D]. Query i of a sequence with lq queries sees keys j <= lk - lq + i
 // with causal (the mask aligned to the bottom right), all lk keys otherwise. Head h reads kv head h / (Hq / Hkv).
 //
-// One block per (64-query tile, sequence, pair of q heads of one kv head -- or one head when Hq / Hkv is odd), 4
-// waves per head; wave w of a head owns queries 16w .. 16w+15 of the tile. The two heads share the K/V tiles (half
+// One block per (128-query tile, sequence, pair of q heads of one kv head -- or one head when Hq / Hkv is odd), 4
+// waves per head; wave w of a head owns queries 32w .. 32w+31 of the tile. The two heads share the K/V tiles (half
 // the K/V traffic of a block per head). Per 64-key tile:
 //   1. the K tile goes to LDS key-major ([64][D], 16-byte chunks, rows padded), the V tile dim-major ([D][64],
 //      transposed on the way in, so that a lane's keys of one dim are contiguous);
-//   2. S^T [16 keys x 16 queries] = K Q^T per 16-key subtile with v_mfma_f32_16x16x32_bf16 (K rows from LDS as the
-//      A operand, the wave's Q rows from registers as the B operand): lane l holds keys 4 (l / 16) + r of query
-//      l % 16;
-//   3. fp32 online softmax in base 2 (scale * log2 e folded in) per query (a 4-register max and two lane swaps);
-//   4. O^T [16 dims x 16 queries] += V^T P^T per 16-dim tile and 32-key step: P (bf16) stays in the registers it was
-//      computed in as the B operand, whose 8 k slots of lane l are the keys 4 (l / 16) .. +3 and 16 + 4 (l / 16) ..
-//      +3 of the step; the A operand reads the same keys of dim l % 16 from the transposed V tile (two 8-byte LDS
+//   2. S^T [32 keys x 32 queries] = K Q^T per 32-key half with v_mfma_f32_32x32x16_bf16 (K rows from LDS as the A
+//      operand, the wave's Q rows from registers as the B operand): lane l holds keys 8 (r / 4) + 4 (l / 32) + r % 4
+//      (register r) of query l % 32, so one query's 64 scores sit in lanes l and l ^ 32;
+//   3. fp32 online softmax in base 2 per query: the max of the raw scores, then p = 2^(s * scale * log2 e - m) in
+//      one FMA and the hardware exp;
+//   4. O^T [32 dims x 32 queries] += V^T P^T per 32-dim tile and 16-key step: P (bf16) stays in the registers it was
+//      computed in as the B operand, whose 8 k slots of lane l are the keys 4 (l / 32) .. +3 and 8 + 4 (l / 32) ..
+//      +3 of the step; the A operand reads the same keys of dim l % 32 from the transposed V tile (two 8-byte LDS
 //      reads). Each lane keeps one query's O, so the rescale by 2^(m_old - m_new) is lane-local.
-// P is rounded to bf16 for the P.V product (as flash-attn does); scores, softmax and O are fp32; output bf16.
+// A wave's 32 queries use each K and V fragment it reads from LDS twice as often as 16 would, which halves the LDS
+// reads per flop; the per-tile work that does not scale with the queries (loads, LDS stores, barriers) is shared by
+// twice the flops.
+// P is rounded to bf16 for the P.V product (as flash-attn does) and the row sum adds the fp32 p (as flash-attn
+// does); scores, softmax and O are fp32; output bf16. The softmax scale must be positive.
 #include <algorithm>
 
 #include "common.h"
@@ -32,8 +37,9 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBQ = 64;   // queries per block
+constexpr int kBQ = 128;  // queries per block and head (4 waves x 32)
 constexpr int kBK = 64;   // keys per tile
 constexpr int kThreads = 256;
 
@@ -47,7 +53,7 @@ struct PrefillArgs {
   const int32_t* bt;  // [num_seqs, max_blocks] or null
   int64_t q_st, q_sh, k_st, v_st, o_st, o_sh;
   int Hkv, G, bs, num_blocks, max_blocks;
-  float scale_log2;
+  float scale_log2;  // softmax scale * log2(e), > 0
   int causal;
   int qtiles, nhg;  // query tiles per sequence (from max_seqlen_q), head groups (Hq / heads per block)
 };
@@ -63,14 +69,14 @@ __device__ __forceinline__ int64_t key_row(const PrefillArgs& g, int k0s, int j,
 
 // HB q heads of one kv head per block (4 waves each, sharing the K/V tiles in LDS).
 template <int D, bool PAGED, int HB>
-__global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const PrefillArgs g) {
-  constexpr int KC = D / 32;   // 32-wide dim steps of Q.K
-  constexpr int DT = D / 16;   // 16-dim output tiles
+__global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(const PrefillArgs g) {
+  constexpr int DC = D / 16;   // 16-wide dim steps of Q.K
+  constexpr int DT = D / 32;   // 32-dim output tiles
   constexpr int CPR = D / 8;   // 16-byte chunks per K/V row
   constexpr int KP = D + 8;    // K row pitch (elements)
-  constexpr int VP = kBK + 8;  // V^T row pitch
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
+  constexpr int VP = kBK + 4;  // V^T row pitch: the 32 rows of a fragment read start 34 banks apart (no conflict)
+  constexpr int STAGE = kBK * KP + D * VP;  // elements of one LDS stage (K tile, then V^T tile)
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
   // Block order: the ids are dealt round-robin over the 8 XCDs, so consecutive logical ids are taken 8 apart to
   // keep all query tiles of one (sequence, head group) -- which read the same K/V -- on one XCD's L2; within a
@@ -92,26 +98,26 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
     return;
   }
   const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane((tid % kThreads) / 64);
-  const int qi_lane = qt * kBQ + 16 * wave + lane % 16;  // this lane's query (B operand row / O column)
-  const int g4 = lane / 16;
+  const int ql = lane % 32, hf = lane / 32;
+  const int qi_lane = qt * kBQ + 32 * wave + ql;  // this lane's query (B operand column / O column)
 
-  // Q rows of the wave as the B operand: lane l -> query 16 wave + l % 16, dims 32c + 8 (l / 16) .. +8
-  bf16x8_t qf[KC];
+  // Q rows of the wave as the B operand: lane l -> query 32 wave + l % 32, dims 16c + 8 (l / 32) .. +8
+  bf16x8_t qf[DC];
   {
     const bool ok = qi_lane < lq;
-    const uint16_t* qp = g.q + int64_t(q0s + (ok ? qi_lane : 0)) * g.q_st + int64_t(h) * g.q_sh + 8 * g4;
+    const uint16_t* qp = g.q + int64_t(q0s + (ok ? qi_lane : 0)) * g.q_st + int64_t(h) * g.q_sh + 8 * hf;
 #pragma unroll
-    for (int c = 0; c < KC; ++c) qf[c] = ok ? *reinterpret_cast<const bf16x8_t*>(qp + 32 * c) : bf16x8_t{};
+    for (int c = 0; c < DC; ++c) qf[c] = ok ? *reinterpret_cast<const bf16x8_t*>(qp + 16 * c) : bf16x8_t{};
   }
   const int diag = lk - lq;  // query i sees keys <= diag + i
   const int q_last = min(qt * kBQ + kBQ, lq) - 1;
   const int k_end = g.causal ? min(lk, diag + q_last + 1) : lk;  // keys this block needs
   const int limit_lane = g.causal ? diag + qi_lane : lk - 1;      // last key of this lane's query
-  const int wave_q0 = qt * kBQ + 16 * wave;                        // the wave's first query
+  const int wave_q0 = qt * kBQ + 32 * wave;                        // the wave's first query
 
-  f32x4_t o[DT];
+  f32x16_t o[DT];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) o[t] = f32x4_t{0, 0, 0, 0};
+  for (int t = 0; t < DT; ++t) o[t] = f32x16_t{};
   float m_run = -INFINITY, l_run = 0.0f;
 
   // 1. a tile's K and V chunks go global -> registers (all loads of a tile issued together; the next tile's loads
@@ -150,7 +156,9 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
       R.v[i] = *reinterpret_cast<const u32x4*>(vrow >= 0 ? g.v + vrow + (c / kBK) * 8 : g.q);
     }
   };
-  auto lstore = [&](const Regs& R) {
+  auto lstore = [&](const Regs& R, int stage) {
+    uint16_t* Ks = lds + stage * STAGE;
+    uint16_t* Vt = Ks + kBK * KP;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * NT;
@@ -163,100 +171,110 @@ __global__ __launch_bounds__(kThreads * HB) void prefill_attention_kernel(const 
     }
   };
 
-  auto tile = [&](int kt0) {
-    // 2. S^T per 16-key subtile: lane holds keys kt0 + 16 st + 4 g4 + r of query qi_lane
-    f32x4_t s[4];
+  // 2.-4. per 32-key half u of a tile: S^T, online softmax, O^T += V^T P^T. The two halves are separate softmax
+  // steps so that the VALU work of one overlaps the MFMAs of the other. Rescaling is lazy: a query's reference max
+  // m_run only moves when a score exceeds it by more than kLazy (base 2), so p <= 2^kLazy; O and the row sum carry
+  // the same factor, which cancels in O / sum, and almost every tile after the first skips the O rescale.
+  constexpr float kLazy = 8.0f;
+  auto tile = [&](int kt0, int stage) {
+    const uint16_t* Ks = lds + stage * STAGE;
+    const uint16_t* Vt = Ks + kBK * KP;
+    // S^T per 32-key half: lane holds keys kt0 + 32 u + 8 (r / 4) + 4 hf + r % 4 of query qi_lane
+    f32x16_t s[2];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      s[st] = f32x4_t{0, 0, 0, 0};
-      const uint16_t* kr = &Ks[(16 * st + lane % 16) * KP + 8 * g4];
+    for (int u = 0; u < 2; ++u) {
+      s[u] = f32x16_t{};
+      const uint16_t* kr = &Ks[(32 * u + ql) * KP + 8 * hf];
 #pragma unroll
-      for (int c = 0; c < KC; ++c)
-        s[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(kr + 32 * c), qf[c], s[st],
-                                                        0, 0, 0);
+      for (int c = 0; c < DC; ++c)
+        s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8_t*>(kr + 16 * c), qf[c], s[u],
+                                                       0, 0, 0);
     }
-    // 3. online softmax of query qi_lane over this tile. Only a tile that reaches past the key count or past the
-    // causal limit of the wave's first query needs the mask (wave-uniform test). 2^x is the hardware v_exp_f32:
-    // its arguments are <= 0 here and only results below the fp32 normal range (which flush to 0) differ from exp2f.
+    // Only a tile that reaches past the key count or past the causal limit of the wave's first query needs the
+    // mask (wave-uniform test); key offsets within the tile are compile-time constants per register.
     const bool full = kt0 + kBK <= lk && (!g.causal || kt0 + kBK - 1 <= diag + wave_q0);
-    float tmax = -INFINITY;
+    const int lim = min(lk - 1, limit_lane) - kt0 - 4 * hf;  // largest visible offset 32 u + 8 (r / 4) + r % 4
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
+    for (int u = 0; u < 2; ++u) {
+      if (!full) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = kt0 + 16 * st + 4 * g4 + r;
-        const float v = (full || (j < lk && j <= limit_lane)) ? s[st][r] * g.scale_log2 : -INFINITY;
-        s[st][r] = v;
-        tmax = fmaxf(tmax, v);
+        for (int r = 0; r < 16; ++r)
+          if (32 * u + 8 * (r / 4) + r % 4 > lim) s[u][r] = -INFINITY;
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    if (__ballot(m_new != m_run) != 0) {  // some row's max moved: rescale (most later tiles skip this)
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      l_run *= alpha;
+      // max of the raw scores (the scale is positive), then p = 2^(s * scale_log2 - m) in one FMA and v_exp_f32
+      // (arguments <= kLazy; only results below the fp32 normal range, which flush to 0, differ from exp2f)
+      float tmax = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) o[t] *= alpha;
-    }
-    m_run = m_new;
-    // p as bf16, packed per 32-key step in the k-slot order of the P.V product
-    bf16x8_t pf[2];
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * g.scale_log2;
+      const bool move = tmax > m_run + kLazy;  // also true for the first finite max (m_run = -inf)
+      if (__ballot(move) != 0) {
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.0f;  // 0 from m_run = -inf
+        if (move) m_run = tmax;
+        l_run *= alpha;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      float p[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(s[2 * m][r] - m_use);
-        p[4 + r] = __builtin_amdgcn_exp2f(s[2 * m + 1][r] - m_use);
+        for (int t = 0; t < DT; ++t) o[t] *= alpha;
       }
-      const u32x4 pk = pack8(p);
-      float pr[8];
-      unpack8(pk, pr);  // the sum uses the bf16 values that enter P.V
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+      // p as bf16, packed per 16-key step (registers 8 j .. 8 j + 7) in the k-slot order of P.V
+      bf16x8_t pf[2];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) l_run += pr[e];
-      pf[m] = __builtin_bit_cast(bf16x8_t, pk);
-    }
-    // 4. O^T += V^T P^T: A = V^T rows (dim 16 t + l % 16), keys 32m + 4 g4 .. +3 and 32m + 16 + 4 g4 .. +3
+      for (int j = 0; j < 2; ++j) {
+        float p[8];
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const uint16_t* vr = &Vt[(16 * t + lane % 16) * VP + 4 * g4];
+        for (int e = 0; e < 8; ++e) {
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][8 * j + e], g.scale_log2, -m_use));
+          l_run += p[e];
+        }
+        pf[j] = __builtin_bit_cast(bf16x8_t, pack8(p));
+      }
+      // O^T += V^T P^T: A = V^T rows (dim 32 t + l % 32), keys 32 u + 16 j + 4 hf .. +3 and .. + 8 .. +3
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + 32 * m);
-        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 32 * m + 16);
-        const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pf[m], o[t], 0, 0, 0);
+      for (int t = 0; t < DT; ++t) {
+        const uint16_t* vr = &Vt[(32 * t + ql) * VP + 32 * u + 4 * hf];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + 16 * j);
+          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 16 * j + 8);
+          const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pf[j], o[t], 0, 0, 0);
+        }
       }
     }
   };
-  // The next tile's loads are issued into the register set right after it has been stored to LDS, so they are in
-  // flight while this tile is computed (past the last tile the last one is loaded again, unused; every load is
-  // issued unconditionally so the compiler's waits are exact). Two tiles ahead measured no faster.
+  // Two LDS stages: while the waves compute tile i from one, the loads of tile i + 1 (issued a tile earlier) are
+  // stored into the other and the loads of tile i + 2 are issued; one barrier per tile. Past the last tile the last
+  // one is loaded and stored again, unused (every load is issued unconditionally so the compiler's waits are exact).
   if (k_end > 0) {
     const int last = (k_end - 1) / kBK * kBK;
     Regs A;
     gload(A, 0);
+    lstore(A, 0);
+    __syncthreads();
+    gload(A, min(kBK, last));
+    int stage = 0;
     for (int kt0 = 0; kt0 < k_end; kt0 += kBK) {
-      lstore(A);
+      tile(kt0, stage);
+      lstore(A, stage ^ 1);
+      gload(A, min(kt0 + 2 * kBK, last));
       __syncthreads();
-      gload(A, min(kt0 + kBK, last));
-      tile(kt0);
-      __syncthreads();  // the LDS tiles are rewritten next
+      stage ^= 1;
     }
   }
 
-  // row sums over the 4 lane groups of the query; lane l holds O^T dims 16 t + 4 g4 + r of query qi_lane
-  l_run += __shfl_xor(l_run, 16);
+  // row sums over the two lane halves of the query; lane l holds O^T dims 32 t + 8 (r / 4) + 4 hf + r % 4 of query
+  // qi_lane
   l_run += __shfl_xor(l_run, 32);
   if (qi_lane >= lq) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  uint16_t* op = g.out + int64_t(q0s + qi_lane) * g.o_st + int64_t(h) * g.o_sh + 4 * g4;
+  uint16_t* op = g.out + int64_t(q0s + qi_lane) * g.o_st + int64_t(h) * g.o_sh + 4 * hf;
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    *reinterpret_cast<u32x2_t*>(op + 16 * t) =
-        u32x2_t{pack_bf16x2(o[t][0] * inv, o[t][1] * inv), pack_bf16x2(o[t][2] * inv, o[t][3] * inv)};
-  }
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+      *reinterpret_cast<u32x2_t*>(op + 32 * t + 8 * rr) =
+          u32x2_t{pack_bf16x2(o[t][4 * rr] * inv, o[t][4 * rr + 1] * inv),
+                  pack_bf16x2(o[t][4 * rr + 2] * inv, o[t][4 * rr + 3] * inv)};
 }
 
 }  // namespace
@@ -273,6 +291,7 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   using namespace nvhip;
   clear_error();
   if (num_seqs < 0 || max_seqlen_q < 0 || Hq < 1 || Hkv < 1) return invalid("prefill_attention: bad size");
+  if (!(scale > 0.0f) || scale == INFINITY) return invalid("prefill_attention: softmax_scale must be positive");
   if (Hq % Hkv != 0) return invalid("prefill_attention: Hq must be a multiple of Hkv");
   if (D != 64 && D != 128) return invalid("prefill_attention: head_dim must be 64 or 128");
   if (q_stride_head < D || q_stride_token < Hq * q_stride_head || out_stride_head < D ||

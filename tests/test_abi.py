@@ -112,14 +112,16 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
 
     pre = lib.nvhip_prefill_attention_bf16
 
-    def prefill(num_seqs=2, maxq=64, Hq=16, Hkv=8, D=128, kst=4160, bt=None, bs=0, nb=0, mb=0):
+    def prefill(num_seqs=2, maxq=64, Hq=16, Hkv=8, D=128, kst=4160, bt=None, bs=0, nb=0, mb=0, scale=0.1):
         return pre(P, P, P, P, P, P, num_seqs, maxq, Hq, Hkv, D, 4160, 128, kst, kst, 2048, 128, bt, bs, nb, mb,
-                   0.1, 1, P)
+                   scale, 1, P)
 
     assert prefill(D=256) == _lib.NVHIP_EINVAL and "head_dim" in _err()
     assert prefill(kst=1000) == _lib.NVHIP_EINVAL and "k / v strides" in _err()
     assert prefill(bt=ctypes.c_void_p(64), bs=0) == _lib.NVHIP_EINVAL and "block table" in _err()
     assert prefill(maxq=0) == _lib.NVHIP_OK
+    assert prefill(scale=0.0) == _lib.NVHIP_EINVAL and "softmax_scale" in _err()
+    assert prefill(scale=-0.1) == _lib.NVHIP_EINVAL and "softmax_scale" in _err()
     assert prefill() == _lib.NVHIP_EINVAL and "null" in _err()
 
     st = lib.nvhip_store_kvcache
