@@ -49,6 +49,18 @@ __device__ __forceinline__ float round_bf16(float a) { return bf16_lo(pack_bf16x
 // and the GEMM epilogue that fuses it, so both give the same bits.
 __device__ __forceinline__ float silu_bf16(float g) { return round_bf16(g / (1.0f + expf(-g))); }
 
+// max / sum of v over lanes l and l ^ 32 of the wave, the same bits in both lanes: v_permlane32_swap of v with
+// itself returns lanes 0..31 of v in one result and lanes 32..63 in the other (in every lane), a VALU op with no
+// LDS round trip.
+__device__ __forceinline__ float pair32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // 8 bf16 (16 bytes) <-> 8 fp32.
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 #pragma unroll

@@ -179,17 +179,45 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
   auto tile = [&](int kt0, int stage) {
     const uint16_t* Ks = lds + stage * STAGE;
     const uint16_t* Vt = Ks + kBK * KP;
-    // S^T per 32-key half: lane holds keys kt0 + 32 u + 8 (r / 4) + 4 hf + r % 4 of query qi_lane
+    // S^T per 32-key half: lane holds keys kt0 + 32 u + 8 (r / 4) + 4 hf + r % 4 of query qi_lane. All K fragments
+    // of the tile are read before the first MFMA, so the MFMAs wait for LDS latency once, not once each.
+    bf16x8_t kf[2][DC];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+        kf[u][c] = *reinterpret_cast<const bf16x8_t*>(&Ks[(32 * u + ql) * KP + 8 * hf + 16 * c]);
     f32x16_t s[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       s[u] = f32x16_t{};
-      const uint16_t* kr = &Ks[(32 * u + ql) * KP + 8 * hf];
 #pragma unroll
-      for (int c = 0; c < DC; ++c)
-        s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8_t*>(kr + 16 * c), qf[c], s[u],
-                                                       0, 0, 0);
+      for (int c = 0; c < DC; ++c) s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[u][c], qf[c], s[u], 0, 0, 0);
     }
+    // V^T fragments of both halves (A operands of O^T += V^T P^T): dim 32 t + l % 32, keys 32 u + 16 j + 4 hf .. +3
+    // and 32 u + 16 j + 8 + 4 hf .. +3; read here so that they are in flight during the softmax
+    u32x4 vf[2][DT][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint16_t* vr = &Vt[(32 * t + ql) * VP + 32 * u + 16 * j + 4 * hf];
+          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
+          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 8);
+          vf[u][t][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+    // issue order: the 8 K reads of half 0, then its MFMAs each followed by a K read of half 1, the MFMAs of half 1,
+    // then the V reads
+    __builtin_amdgcn_sched_group_barrier(0x100, DC, 0);
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, DC, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4 * DT, 0);
     // Only a tile that reaches past the key count or past the causal limit of the wave's first query needs the
     // mask (wave-uniform test); key offsets within the tile are compile-time constants per register.
     const bool full = kt0 + kBK <= lk && (!g.causal || kt0 + kBK - 1 <= diag + wave_q0);
@@ -206,7 +234,7 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
       float tmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * g.scale_log2;
+      tmax = pair32_max(tmax) * g.scale_log2;
       const bool move = tmax > m_run + kLazy;  // also true for the first finite max (m_run = -inf)
       if (__ballot(move) != 0) {
         const float alpha = move ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.0f;  // 0 from m_run = -inf
@@ -228,18 +256,13 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
         }
         pf[j] = __builtin_bit_cast(bf16x8_t, pack8(p));
       }
-      // O^T += V^T P^T: A = V^T rows (dim 32 t + l % 32), keys 32 u + 16 j + 4 hf .. +3 and .. + 8 .. +3
+      // O^T += V^T P^T
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const uint16_t* vr = &Vt[(32 * t + ql) * VP + 32 * u + 4 * hf];
+      for (int t = 0; t < DT; ++t)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr + 16 * j);
-          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 16 * j + 8);
-          const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pf[j], o[t], 0, 0, 0);
-        }
-      }
+        for (int j = 0; j < 2; ++j)
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[u][t][j]), pf[j], o[t], 0, 0,
+                                                         0);
     }
   };
   // Two LDS stages: while the waves compute tile i from one, the loads of tile i + 1 (issued a tile earlier) are
@@ -264,7 +287,7 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
 
   // row sums over the two lane halves of the query; lane l holds O^T dims 32 t + 8 (r / 4) + 4 hf + r % 4 of query
   // qi_lane
-  l_run += __shfl_xor(l_run, 32);
+  l_run = pair32_sum(l_run);
   if (qi_lane >= lq) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
   uint16_t* op = g.out + int64_t(q0s + qi_lane) * g.o_st + int64_t(h) * g.o_sh + 4 * hf;
