@@ -78,13 +78,22 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
   constexpr int STAGE = kBK * KP + D * VP;  // elements of one LDS stage (K tile, then V^T tile)
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
-  // Block order: the ids are dealt round-robin over the 8 XCDs, so consecutive logical ids are taken 8 apart to
-  // keep all query tiles of one (sequence, head group) -- which read the same K/V -- on one XCD's L2; within a
-  // group the query tiles run from the last (the most keys) to the first.
-  int lid = blockIdx.x;
-  const int nblk = gridDim.x;
-  if (nblk % 8 == 0) lid = (lid % 8) * (nblk / 8) + lid / 8;
-  const int grp = lid / g.qtiles, qt = g.qtiles - 1 - lid % g.qtiles;
+  // Block order. The ids are dealt round-robin over the 8 XCDs (block b runs on XCD b % 8) and each XCD starts its
+  // blocks in id order as CUs free up. When the groups (sequence, head group) divide evenly, XCD x takes whole
+  // groups -- all query tiles of a group read the same K/V, which then stays in one XCD's L2 -- and starts them
+  // heaviest query tile (most keys) first across its groups, so that no long tile starts late (longest-first list
+  // scheduling; starting one group's tiles before the next group's left a third of the CUs idle at the end of a
+  // 4 x 2048-token prefill). Otherwise all groups' tiles are dealt heaviest first.
+  const int nblk = gridDim.x, ngrp = nblk / g.qtiles;
+  int grp, qt;
+  if (nblk % 8 == 0 && (nblk / 8) % g.qtiles == 0) {
+    const int gx = nblk / 8 / g.qtiles, r = blockIdx.x / 8;
+    grp = (blockIdx.x % 8) * gx + r % gx;
+    qt = g.qtiles - 1 - r / gx;
+  } else {
+    grp = blockIdx.x % ngrp;
+    qt = g.qtiles - 1 - blockIdx.x / ngrp;
+  }
   const int b = grp / g.nhg, hg = grp % g.nhg;
   const int h = hg * HB + int(threadIdx.x) / kThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
