@@ -8,9 +8,9 @@
 // paged caches [num_blocks, block_size, Hkv, D]. Query i of a sequence with lq queries sees keys j <= lk - lq + i
 // with causal (the mask aligned to the bottom right), all lk keys otherwise. Head h reads kv head h / (Hq / Hkv).
 //
-// One block per (128-query tile, sequence, pair of q heads of one kv head -- or one head when Hq / Hkv is odd), 4
-// waves per head; wave w of a head owns queries 32w .. 32w+31 of the tile. The two heads share the K/V tiles (half
-// the K/V traffic of a block per head). Per 64-key tile:
+// One block (8 waves) per (query tile, sequence, pair of q heads of one kv head): 4 waves and 128 queries per head;
+// when Hq / Hkv is odd, one head per block with 8 waves and 256 queries. Wave w of a head owns queries 32w .. 32w+31
+// of the tile. The two heads share the K/V tiles (half the K/V traffic of a block per head). Per 64-key tile:
 //   1. the K tile goes to LDS key-major ([64][D], 16-byte chunks, rows padded), the V tile dim-major ([D][64],
 //      transposed on the way in, so that a lane's keys of one dim are contiguous);
 //   2. S^T [32 keys x 32 queries] = K Q^T per 32-key half with v_mfma_f32_32x32x16_bf16 (K rows from LDS as the A
@@ -39,9 +39,11 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBQ = 128;  // queries per block and head (4 waves x 32)
+constexpr int kWavesBlock = 8;  // waves per block: 4 per head with two heads, 8 with one
 constexpr int kBK = 64;   // keys per tile
-constexpr int kThreads = 256;
+constexpr int kThreads = 64 * kWavesBlock;
+// queries per block and head (32 per wave)
+__host__ __device__ constexpr int block_queries(int heads_per_block) { return 32 * kWavesBlock / heads_per_block; }
 
 struct PrefillArgs {
   uint16_t* out;
@@ -69,7 +71,8 @@ __device__ __forceinline__ int64_t key_row(const PrefillArgs& g, int k0s, int j,
 
 // HB q heads of one kv head per block (4 waves each, sharing the K/V tiles in LDS).
 template <int D, bool PAGED, int HB>
-__global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(const PrefillArgs g) {
+__global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const PrefillArgs g) {
+  constexpr int kBQ = block_queries(HB), kHeadThreads = kThreads / HB;
   constexpr int DC = D / 16;   // 16-wide dim steps of Q.K
   constexpr int DT = D / 32;   // 32-dim output tiles
   constexpr int CPR = D / 8;   // 16-byte chunks per K/V row
@@ -95,18 +98,18 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
     qt = g.qtiles - 1 - blockIdx.x / ngrp;
   }
   const int b = grp / g.nhg, hg = grp % g.nhg;
-  const int h = hg * HB + int(threadIdx.x) / kThreads, kvh = (hg * HB) / g.G;
+  const int h = hg * HB + int(threadIdx.x) / kHeadThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
   if (qt * kBQ >= lq || lk <= 0) {
-    const int r = int(threadIdx.x) % kThreads;
+    const int r = int(threadIdx.x) % kHeadThreads;
     if (qt * kBQ < lq && r < kBQ && qt * kBQ + r < lq) {  // no keys: zero rows
       uint16_t* o = g.out + int64_t(q0s + qt * kBQ + r) * g.o_st + int64_t(h) * g.o_sh;
       for (int d = 0; d < D; ++d) o[d] = 0;
     }
     return;
   }
-  const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane((tid % kThreads) / 64);
+  const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane((tid % kHeadThreads) / 64);
   const int ql = lane % 32, hf = lane / 32;
   const int qi_lane = qt * kBQ + 32 * wave + ql;  // this lane's query (B operand column / O column)
 
@@ -134,25 +137,48 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
   // chunk c: key c % 64, dims (c / 64) * 8, stored transposed (a wave's lanes take consecutive keys of one dim
   // chunk, so the 2-byte LDS writes of a lane group are contiguous). Invalid keys read the first 16 bytes of q and
   // store zeros.
-  constexpr int NT = kThreads * HB;         // threads loading the tiles
+  constexpr int NT = kThreads;              // threads loading the tiles
   constexpr int NL = kBK * CPR / NT;        // chunks per thread per operand
   static_assert(NL >= 1 && NL * NT == kBK * CPR, "tile chunks per thread");
   struct Regs {
     u32x4 k[NL], v[NL];
     uint32_t kok, vok;
+    bool all;  // every key of the tile is valid (wave-uniform): no zeroing at the LDS store
   };
   const int32_t* bt_row = PAGED ? g.bt + int64_t(b) * g.max_blocks : nullptr;
+  // Contiguous keys: this thread's K / V row addresses at key tile 0; tile kt0 adds kt0 rows (a scalar offset).
+  const uint16_t* kbase[NL];
+  const uint16_t* vbase = nullptr;
+  if constexpr (!PAGED) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int c = tid + i * NT;
+      kbase[i] = g.k + int64_t(k0s + c / CPR) * g.k_st + int64_t(kvh) * D + (c % CPR) * 8;
+    }
+    vbase = g.v + int64_t(k0s + tid % kBK) * g.v_st + int64_t(kvh) * D;
+  }
   auto gload = [&](Regs& R, int kt0) {
+    const int vj = kt0 + tid % kBK;  // V chunks of a thread share one key (NT is a multiple of kBK)
+    R.all = kt0 + kBK <= lk;
+    R.kok = R.vok = 0;
+    if constexpr (!PAGED) {
+      if (R.all) {  // every row valid: the addresses are the bases plus a per-tile offset
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          R.k[i] = *reinterpret_cast<const u32x4*>(kbase[i] + int64_t(kt0) * g.k_st);
+          R.v[i] = *reinterpret_cast<const u32x4*>(vbase + int64_t(kt0) * g.v_st + ((tid + i * NT) / kBK) * 8);
+        }
+        return;
+      }
+    }
     // block-table entries of this thread's keys first (PAGED), then every data load back to back
     int kblk[NL], vblk = 0;
-    const int vj = kt0 + tid % kBK;  // V chunks of a thread share one key (NT is a multiple of kBK)
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int kj = kt0 + (tid + i * NT) / CPR;
       kblk[i] = PAGED && kj < lk ? bt_row[kj / g.bs] : 0;
     }
     if constexpr (PAGED) vblk = vj < lk ? bt_row[vj / g.bs] : 0;
-    R.kok = R.vok = 0;
     const int64_t vrow = vj < lk ? key_row<D, PAGED>(g, k0s, vj, vblk, kvh, g.v_st) : -1;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -164,16 +190,18 @@ __global__ __launch_bounds__(kThreads * HB, 2) void prefill_attention_kernel(con
       R.k[i] = *reinterpret_cast<const u32x4*>(krow >= 0 ? g.k + krow + (c % CPR) * 8 : g.q);
       R.v[i] = *reinterpret_cast<const u32x4*>(vrow >= 0 ? g.v + vrow + (c / kBK) * 8 : g.q);
     }
+    if constexpr (PAGED) R.all = false;  // a block-table entry may be invalid
   };
   auto lstore = [&](const Regs& R, int stage) {
     uint16_t* Ks = lds + stage * STAGE;
     uint16_t* Vt = Ks + kBK * KP;
+    const bool all = R.all;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * NT;
       const u32x4 zero = u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&Ks[(c / CPR) * KP + (c % CPR) * 8]) = ((R.kok >> i) & 1) ? R.k[i] : zero;
-      const u32x4 x = ((R.vok >> i) & 1) ? R.v[i] : zero;
+      *reinterpret_cast<u32x4*>(&Ks[(c / CPR) * KP + (c % CPR) * 8]) = (all || ((R.kok >> i) & 1)) ? R.k[i] : zero;
+      const u32x4 x = (all || ((R.vok >> i) & 1)) ? R.v[i] : zero;
       const int key = c % kBK, dc = (c / kBK) * 8;
 #pragma unroll
       for (int e = 0; e < 8; ++e) Vt[(dc + e) * VP + key] = uint16_t(x[e / 2] >> (16 * (e & 1)));
@@ -339,7 +367,8 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   if (!out || !q || !k || !v || !cu_seqlens_q || !cu_seqlens_k) return invalid("prefill_attention: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || reinterpret_cast<uintptr_t>(out) % 8)
     return invalid("prefill_attention: q, k, v must be 16-byte and out 8-byte aligned");
-  const int64_t qtiles = (max_seqlen_q + kBQ - 1) / kBQ;
+  const int hb = (Hq / Hkv) % 2 == 0 ? 2 : 1;  // q heads per block
+  const int64_t qtiles = (max_seqlen_q + block_queries(hb) - 1) / block_queries(hb);
   if (qtiles > INT32_MAX || num_seqs > INT32_MAX || num_blocks > INT32_MAX ||
       max_blocks * block_size > INT32_MAX)
     return invalid("prefill_attention: size too large");
@@ -365,12 +394,11 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
                 causal ? 1 : 0,
                 0,
                 0};
-  const int hb = (Hq / Hkv) % 2 == 0 ? 2 : 1;  // q heads per block
   g.qtiles = int(qtiles);
   g.nhg = int(Hq / hb);
   const int64_t blocks = qtiles * num_seqs * (Hq / hb);
   if (blocks > INT32_MAX) return invalid("prefill_attention: size too large");
-  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kThreads * hb));
+  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kThreads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool paged = block_table != nullptr;
 #define NVHIP_PREFILL_LAUNCH(DD, PG, HBV) hipLaunchKernelGGL((prefill_attention_kernel<DD, PG, HBV>), grid, block, 0, s, g)

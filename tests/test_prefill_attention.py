@@ -96,6 +96,13 @@ def test_head_dim_64_and_gqa():
         check(q.contiguous(), k.contiguous(), v.contiguous(), cu([90, 200]), cu([90, 200]))
 
 
+def test_odd_group_size_one_head_per_block():
+    # Hq / Hkv odd: one q head per block, 256-query tiles; lengths past one and two tiles
+    for Hq, Hkv, D, lens in [(6, 2, 128, [600, 37]), (3, 1, 64, [257, 513])]:
+        _, q, k, v = contiguous_case(lens, Hq=Hq, Hkv=Hkv, D=D, seed=Hq * 7 + D)
+        check(q.contiguous(), k.contiguous(), v.contiguous(), cu(lens), cu(lens))
+
+
 def test_non_causal_and_more_queries_than_keys():
     _, q, k, v = contiguous_case([50, 120], seed=3)
     check(q.contiguous(), k.contiguous(), v.contiguous(), cu([50, 120]), cu([50, 120]), causal=False)
