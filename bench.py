@@ -268,7 +268,7 @@ def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
             "context_tokens": ctx, "bytes": nbytes}
 
 
-def prefill_attention(torch, dev, steps, g, nseq=4, L=2048):
+def prefill_attention(torch, dev, steps, g, nseq=4, L=2048, profile=False):
     """Causal prefill attention of one Qwen3-0.6B layer over nseq sequences of L tokens (k, v views of the qkv
     output). flops = 4 * D * Hq * sum over queries of the keys each sees (L (L + 1) / 2 per sequence)."""
     from nanovllm_hip.kernels.attention import flash_attn_varlen_func
@@ -278,6 +278,12 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048):
     k = buf[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D)
     v = buf[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].view(T, HKV, D)
     cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=dev)
+    if profile:  # for a rocprofv3 kernel trace: `steps` eager launches, nothing else launched
+        for _ in range(steps):
+            flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True)
+        torch.cuda.synchronize()
+        print(f"profile: {steps} prefill attention launches ({nseq} x {L} tokens)", flush=True)
+        return None
     ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True), 4,
                        max(20, steps // 4), 4, WARM_S)
     flops = 4 * D * HQ * nseq * L * (L + 1) // 2
@@ -380,6 +386,9 @@ def main():
     p.add_argument("--profile-e2e", action="store_true",
                    help="for rocprofv3 kernel traces: build the Qwen3-0.6B-shaped model, prefill, capture the batch-32 "
                         "decode step and replay it --steps times, then print the e2e line")
+    p.add_argument("--profile-prefill", action="store_true",
+                   help="for rocprofv3 kernel traces: --steps eager launches of the prefill attention (4 x 2048 "
+                        "tokens, one Qwen3-0.6B layer)")
     p.add_argument("--profile", action="store_true",
                    help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
                         "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
@@ -398,6 +407,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.profile_gemm:
         profile_gemm(torch, kernels, dev, args.steps, args.gemm_m)
+        return
+    if args.profile_prefill:
+        prefill_attention(torch, dev, args.steps, torch.Generator().manual_seed(0), profile=True)
         return
     if args.profile_e2e:
         print(json.dumps(e2e_decode_step(torch, dev, profile_replays=args.steps)), flush=True)
