@@ -15,12 +15,19 @@
 //      each group of 4 tokens);
 //   2. computes S^T [16 tokens x 16 rows] = K Q^T per tile with v_mfma_f32_16x16x32_bf16 (Q rows as the B operand,
 //      held in registers; rows >= R are zero), so lane l holds tokens 4 (l / 16) + r of row l % 16;
-//   3. updates the row's running max (fp32, base-2 exponent with the scale folded in), turns the scores into
-//      p = 2^(s - max) and hands p and the rescale factor of each row to the other lanes through the wave's own LDS
-//      slice;
-//   4. accumulates O[row][dims] = O * rescale + sum p * V in fp32 with the lane-owns-8-dims layout of step 1.
-// At the end the 4 token groups of a wave are summed with lane shuffles and the 8 waves' (max, sum, O) are merged
-// through LDS in wave order (deterministic), O / sum rounded to bf16.
+//   3. updates the row's running max (fp32, base-2 exponent with the scale folded into one FMA; lazy: the
+//      reference max moves only when a score exceeds it by more than 8, so p <= 256 and almost no chunk rescales
+//      O) and turns the scores into p = 2^(s - max) in the registers they were computed in: lane l's 8 values of
+//      row l % 16 are the B operand of the P.V product, as a bf16 head and a bf16 remainder (two MFMAs; p keeps
+//      ~17 bits, where flash-attn rounds it to bf16 once);
+//   4. stores its 32 V rows (row layout: lane l reads dims 8 (l % 16) .. +8 of token l / 16 of each group of 4
+//      tokens) into its own LDS slice and reads them back as the A operand of O^T [16 dims x 16 rows] += V^T P^T
+//      (v_mfma_f32_16x16x32_bf16, one per 16 dims) with the gfx950 transpose read ds_read_b64_tr_b16: within a
+//      16-lane group, lane i receives element i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3),
+//      so lanes addressing 4 consecutive V rows x 16 dims hand each lane 4 tokens of one dim.
+// Lane l keeps O^T dims 16 t + 4 (l / 16) + r of row l % 16, so the rescale is lane-local and no in-wave sum is
+// needed; at the end the 8 waves' (max, sum, O) are merged through LDS in wave order (deterministic), O / sum
+// rounded to bf16.
 // The block-table entries of the block's token range are loaded once, one per lane, alongside the context length
 // and Q.
 // Small batches: with a caller workspace the context of each (sequence, kv head) is split over several blocks
@@ -39,7 +46,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 32;  // tokens per wave step
-constexpr int kWaves = 8;
+constexpr int kWaves = 8;  // waves per block (4 for head_dim 256, whose registers need a whole SIMD per wave)
+__host__ __device__ constexpr int block_waves(int D) { return D == 256 ? 4 : kWaves; }
 
 struct DecodeArgs {
   uint16_t* out;
@@ -53,7 +61,7 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale * log2(e)
   int causal;
   int splits;     // context splits per (sequence, kv head): blocks s = 0 .. splits-1 take tokens
-  int split_len;  // [s * split_len, (s + 1) * split_len); a multiple of kChunk * kWaves
+  int split_len;  // [s * split_len, (s + 1) * split_len); a multiple of kChunk * kWaves (so of kChunk * waves)
   float* ws;      // splits > 1: [num_seqs, Hkv, splits, RP, 2 + D] fp32 records (max, sum, O) of each block
 };
 
@@ -74,17 +82,31 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
   return ((int64_t(blk) * g.bs + t % g.bs) * g.Hkv + kvh) * D;
 }
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 4 bf16 of the A operand from a row-major tile in LDS (see step 4): the 8-byte chunk this lane addresses is
+// transposed with those of the other lanes of its 16-lane group.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 template <int D, int RP, bool ALIGNED>
-__global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeArgs g) {
-  constexpr int KC = D / 32;         // 32-wide dim chunks of a K row (MFMA k steps)
-  constexpr int LPT = D / 8;         // lanes per V row in the PV layout
-  constexpr int TPI = 64 / LPT;      // tokens per wave instruction in the PV layout
-  constexpr int PVI = kChunk / TPI;  // PV steps per chunk
+__global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const DecodeArgs g) {
+  constexpr int NWV = block_waves(D);
+  constexpr int KC = D / 32;         // 32-wide dim chunks of a K row (MFMA k steps of Q.K)
+  constexpr int LPT = D / 8;         // lanes per V row in the row layout
+  constexpr int TPI = 64 / LPT;      // tokens per wave instruction in the row layout
+  constexpr int PVI = kChunk / TPI;  // V load instructions per chunk
+  constexpr int DT = D / 16;         // 16-dim tiles of O^T
+  constexpr int VPW = D + 16;        // LDS row pitch of a V chunk: the 4 rows of a transpose read hit 32 distinct banks
+  constexpr int KPW = D + 8;         // LDS row pitch of a K chunk: the 16 rows of a fragment read hit distinct banks
   static_assert(D % 32 == 0 && D <= 256 && RP <= 16, "shape");
-  __shared__ float pbuf[kWaves][kChunk][RP];
-  __shared__ float cbuf[kWaves][RP];
-  __shared__ float red_acc[kWaves][RP][D];
-  __shared__ float red_m[kWaves][RP], red_l[kWaves][RP];
+  // LDS: each wave's K and V chunks during the loop, the waves' partial O afterwards (same bytes)
+  constexpr int VBYTES = NWV * kChunk * (VPW + KPW) * 2, RBYTES = NWV * RP * D * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[VBYTES > RBYTES ? VBYTES : RBYTES];
+  __shared__ float red_m[NWV][RP], red_l[NWV][RP];
 
   const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
   const int b = pair / g.Hkv, kvh = pair % g.Hkv;
@@ -113,14 +135,15 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
   // row qrow sees tokens < row_limit
   const int row_limit = qrow >= rows ? 0 : g.causal ? min(max(ctx - g.q_len + qi + 1, 0), ctx) : ctx;
 
-  float m_run = -INFINITY;  // running max of row qrow (the same in the 4 lanes of the row)
+  float m_run = -INFINITY;  // reference max of row qrow (the same in the 4 lanes of the row)
   float l_run = 0.0f;       // this lane's part of the row sum
-  float acc[RP][8];
+  f32x4_t acc[DT];          // O^T dims 16 t + 4 (l / 16) + r of row qrow
 #pragma unroll
-  for (int r = 0; r < RP; ++r)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+  for (int t = 0; t < DT; ++t) acc[t] = f32x4_t{0, 0, 0, 0};
   const int dg = lane % LPT, ts = lane / LPT;
+  const int h4 = lane / 16, l16 = lane % 16;
+  uint16_t* vs = reinterpret_cast<uint16_t*>(smem) + wave * kChunk * (VPW + KPW);  // this wave's V chunk
+  uint16_t* ks = vs + kChunk * VPW;                                                 // and K chunk
   const int tok_end = min(ctx, tok_begin + g.split_len);
   const int ch_end = (tok_end + kChunk - 1) / kChunk;
 
@@ -128,9 +151,8 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
   // by all lanes (a lane whose token is not valid reads the first 16 bytes of q) and the loaded values are used as
   // they are -- invalid tokens are masked out of the scores, so their p is 0 -- so no select waits on a load.
   struct Tile {
-    bf16x8_t k[2][KC];
-    bf16x8_t v[PVI];
-    uint64_t kvalid[2];  // bit j: token t0 + 16u + j has a valid block (from lanes j = 0..15)
+    bf16x8_t k[PVI], v[PVI];  // row layout: dims 8 (l % LPT) .. +8 of token it * TPI + l / LPT
+    uint64_t kvalid[2];       // bit j: token t0 + 16u + j has a valid block (from lanes j = 0..15)
   };
   auto row_of = [&](int t, int64_t base, int t0) -> int64_t {
     if (t >= ctx) return -1;
@@ -146,117 +168,120 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const DecodeA
       base = (blk < 0 || blk >= g.num_blocks) ? -1 : ((int64_t(blk) * g.bs + t0 % g.bs) * g.Hkv + kvh) * D;
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t row = row_of(t0 + 16 * u + lane % 16, base, t0);
-      T.kvalid[u] = __ballot(row >= 0);
-#pragma unroll
-      for (int c = 0; c < KC; ++c) T.k[u][c] = load_bf16x8(row >= 0 ? g.kc + row + 32 * c + q8 : g.q);
-    }
+    for (int u = 0; u < 2; ++u) T.kvalid[u] = __ballot(row_of(t0 + 16 * u + lane % 16, base, t0) >= 0);
 #pragma unroll
     for (int it = 0; it < PVI; ++it) {
       const int64_t row = row_of(t0 + it * TPI + ts, base, t0);
+      T.k[it] = load_bf16x8(row >= 0 ? g.kc + row + 8 * dg : g.q);
       T.v[it] = load_bf16x8(row >= 0 ? g.vc + row + 8 * dg : g.q);
     }
   };
+  constexpr float kLazy = 8.0f;
   auto compute_tile = [&](const Tile& T, int ch) {
     const int t0 = ch * kChunk;
+    // the chunk's K and V rows into this wave's LDS slices (full cache lines were read); the K rows come back as
+    // the A operand of S^T (lane l: token 16u + l % 16, dims 32c + 8 (l / 16) .. +8)
+#pragma unroll
+    for (int it = 0; it < PVI; ++it) {
+      *reinterpret_cast<bf16x8_t*>(ks + (it * TPI + ts) * KPW + 8 * dg) = T.k[it];
+      *reinterpret_cast<bf16x8_t*>(vs + (it * TPI + ts) * VPW + 8 * dg) = T.v[it];
+    }
+    wave_sync();
     // scores: lane holds tokens t0 + 16u + 4 (l / 16) + r of row qrow
     f32x4_t s[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       s[u] = f32x4_t{0, 0, 0, 0};
 #pragma unroll
-      for (int c = 0; c < KC; ++c) s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(T.k[u][c], qf[c], s[u], 0, 0, 0);
+      for (int c = 0; c < KC; ++c)
+        s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            *reinterpret_cast<const bf16x8_t*>(ks + (16 * u + l16) * KPW + 32 * c + 8 * h4), qf[c], s[u], 0, 0, 0);
     }
     float tmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int j = 4 * (lane / 16) + r, t = t0 + 16 * u + j;
-        const bool ok = t < row_limit && ((T.kvalid[u] >> j) & 1);
-        const float v = ok ? s[u][r] * g.scale_log2 : -INFINITY;
-        s[u][r] = v;
-        tmax = fmaxf(tmax, v);
+        const int j = 4 * h4 + r, t = t0 + 16 * u + j;
+        if (!(t < row_limit && ((T.kvalid[u] >> j) & 1))) s[u][r] = -INFINITY;
+        tmax = fmaxf(tmax, s[u][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float resc = exp2f(m_run - m_use);
-    m_run = m_new;
-    l_run *= resc;
+    tmax = pair32_max(tmax) * g.scale_log2;  // the scale is positive
+    const bool move = tmax > m_run + kLazy;  // also true for the first finite max (m_run = -inf)
+    if (__ballot(move) != 0) {
+      const float alpha = move ? exp2f(m_run - tmax) : 1.0f;  // 0 from m_run = -inf
+      if (move) m_run = tmax;
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // P^T as the B operand: k slots 0..3 = tokens 4 h4 + r, 4..7 = tokens 16 + 4 h4 + r, column = row qrow
+    float p[8];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(s[u][r] - m_use);
-        l_run += p;
-        if (qrow < RP) pbuf[wave][16 * u + 4 * (lane / 16) + r][qrow] = p;
+        p[4 * u + r] = exp2f(__builtin_fmaf(s[u][r], g.scale_log2, -m_use));
+        l_run += p[4 * u + r];
       }
-    if (lane < RP) cbuf[wave][lane] = resc;
-    wave_sync();
-    float cr[RP];
+    // p = head + remainder, both bf16: two MFMAs per dim tile keep p to ~2^-17 relative (fp32-like; flash-attn
+    // rounds p to bf16 once)
+    const u32x4 phi = pack8(p);
+    float ph[8];
+    unpack8(phi, ph);
 #pragma unroll
-    for (int r = 0; r < RP; ++r) cr[r] = cbuf[wave][r];
+    for (int e = 0; e < 8; ++e) ph[e] = p[e] - ph[e];
+    const bf16x8_t pk = __builtin_bit_cast(bf16x8_t, phi), pr = __builtin_bit_cast(bf16x8_t, pack8(ph));
+    // V^T fragments with the transpose read: the lanes of group h4 address rows 4 h4 + i / 4 (slots 0..3) and
+    // 16 + 4 h4 + i / 4 (slots 4..7), dims 16 t + 4 (i % 4)
+    const uint16_t* v0 = vs + (4 * h4 + l16 / 4) * VPW + 4 * (l16 % 4);
+    const uint16_t* v1 = v0 + 16 * VPW;
 #pragma unroll
-    for (int r = 0; r < RP; ++r)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r][e] *= cr[r];
-#pragma unroll
-    for (int it = 0; it < PVI; ++it) {
-      const int tok = it * TPI + ts;
-      float pv[RP];
-#pragma unroll
-      for (int r = 0; r < RP; ++r) pv[r] = pbuf[wave][tok][r];
-      float vv[8];
-      unpack8(*reinterpret_cast<const u32x4*>(&T.v[it]), vv);
-#pragma unroll
-      for (int r = 0; r < RP; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][e] = __builtin_fmaf(pv[r], vv[e], acc[r][e]);
+    for (int t = 0; t < DT; ++t) {
+      const u32x2 lo = lds_read_tr16(v0 + 16 * t), hi = lds_read_tr16(v1 + 16 * t);
+      const bf16x8_t va = __builtin_bit_cast(bf16x8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pk, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pr, acc[t], 0, 0, 0);
     }
-    wave_sync();  // pbuf / cbuf are rewritten by the next chunk
+    wave_sync();  // the next chunk rewrites the slice
   };
 
   // The wave's chunks are first, first + 8, ... (issuing two chunks' loads before computing them, or prefetching
   // the next chunk during the current one, measured no faster: a read-only kernel with this access pattern and
   // no compute takes ~35 us where this one takes ~43 us for 163 MB of K/V).
-  for (int ch = tok_begin / kChunk + wave; ch < ch_end; ch += kWaves) {
+  for (int ch = tok_begin / kChunk + wave; ch < ch_end; ch += NWV) {
     Tile A;
     load_tile(A, ch);
     compute_tile(A, ch);
   }
 
-  // sum the TPI token groups (lanes dg + LPT * ts) and the row sums (lanes qrow + 16 * j)
-#pragma unroll
-  for (int off = LPT; off < 64; off *= 2)
-#pragma unroll
-    for (int r = 0; r < RP; ++r)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r][e] += __shfl_xor(acc[r][e], off);
+  // row sums over the 4 lane groups of the row; each lane's O^T values are its own (no in-wave sum)
   l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  if (ts == 0) {
+  l_run = pair32_sum(l_run);
+  __syncthreads();  // every wave is done with its V slice: the partial O reuse those bytes
+  float (*red_acc)[RP][D] = reinterpret_cast<float (*)[RP][D]>(smem);
+  if (qrow < RP) {
 #pragma unroll
-    for (int r = 0; r < RP; ++r)
+    for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red_acc[wave][r][8 * dg + e] = acc[r][e];
-  }
-  if (lane < RP) {
-    red_m[wave][lane] = m_run;
-    red_l[wave][lane] = l_run;
+      for (int r = 0; r < 4; ++r) red_acc[wave][qrow][16 * t + 4 * h4 + r] = acc[t][r];
+    if (h4 == 0) {
+      red_m[wave][qrow] = m_run;
+      red_l[wave][qrow] = l_run;
+    }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < rows * D; idx += kWaves * 64) {
+  for (int idx = threadIdx.x; idx < rows * D; idx += NWV * 64) {
     const int r = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_m[w][r]);
+    for (int w = 0; w < NWV; ++w) M = fmaxf(M, red_m[w][r]);
     float num = 0.0f, den = 0.0f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < NWV; ++w) {
         const float f = exp2f(red_m[w][r] - M);
         num = __builtin_fmaf(red_acc[w][r][d], f, num);
         den = __builtin_fmaf(red_l[w][r], f, den);
@@ -305,7 +330,7 @@ __global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) 
 
 template <int D, int RP>
 int launch_decode(const DecodeArgs& g, int64_t num_seqs, hipStream_t s) {
-  const dim3 grid(unsigned(num_seqs * g.Hkv * g.splits)), block(kWaves * 64);
+  const dim3 grid(unsigned(num_seqs * g.Hkv * g.splits)), block(block_waves(D) * 64);
   if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((paged_decode_kernel<D, RP, false>), grid, block, 0, s, g);
   if (int rc = check_launch("paged_decode_attention")) return rc;
@@ -320,8 +345,7 @@ int launch_decode_rows(const DecodeArgs& g, int64_t num_seqs, int rows, hipStrea
   if (rows <= 2) return launch_decode<D, 2>(g, num_seqs, s);
   if (rows <= 4) return launch_decode<D, 4>(g, num_seqs, s);
   if (rows <= 8) return launch_decode<D, 8>(g, num_seqs, s);
-  if constexpr (D <= 128) return launch_decode<D, 16>(g, num_seqs, s);
-  return invalid("paged_decode_attention: at most 8 query rows per kv head with head_dim 256");
+  return launch_decode<D, 16>(g, num_seqs, s);
 }
 
 int rows_padded(int64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16; }
