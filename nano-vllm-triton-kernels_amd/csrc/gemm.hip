@@ -343,20 +343,23 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
 
 // SILU: W = [gate; up] ([2 * N2, K], N = 2 * N2), C [M, N2]: the block takes gate rows n0 .. and up rows N2 + n0 ..
 // and stores bf16(silu(gate) * up) of the two rounded sums (bitwise the unfused result).
-template <int MT, int NW, int U, bool SILU = false>
+template <int MT, int NCOL, int NW, int U, bool SILU = false>
 __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
   constexpr int NP = SILU ? 2 : 1;  // products per block: (gate, up) or the plain one
+  static_assert(NCOL == 8 || NCOL == 16, "output columns per block");
   __shared__ float red[NW][NP][MT][4][64];
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * NCOL, m0 = blockIdx.y * 16 * MT;
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int fr = lane % 16, fk = (lane / 16) * 8;
   const int nout = SILU ? g.N / 2 : g.N;
+  // with NCOL = 8 the MFMA's columns 8..15 repeat columns 0..7 (same addresses, merged by the memory pipeline)
+  const int wn = min(n0 + fr % NCOL, nout - 1);
   const uint16_t* wrows[NP];
-  wrows[0] = g.w + int64_t(min(n0 + fr, nout - 1)) * g.swn + fk;
-  if constexpr (SILU) wrows[NP - 1] = g.w + int64_t(nout + min(n0 + fr, nout - 1)) * g.swn + fk;
+  wrows[0] = g.w + int64_t(wn) * g.swn + fk;
+  if constexpr (SILU) wrows[NP - 1] = g.w + int64_t(nout + wn) * g.swn + fk;
   const uint16_t* arow[MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) arow[t] = g.a + int64_t(min(t * 16 + fr, g.M - 1)) * g.sam + fk;
+  for (int t = 0; t < MT; ++t) arow[t] = g.a + int64_t(min(m0 + t * 16 + fr, g.M - 1)) * g.sam + fk;
   f32x4_t acc[NP][MT];
 #pragma unroll
   for (int p = 0; p < NP; ++p)
@@ -399,8 +402,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) sum[p] += red[w][p][t][r][l];
     }
-    const int m = t * 16 + 4 * (l / 16) + r, n = n0 + l % 16;
-    if (m >= g.M || n >= nout) continue;
+    const int m = m0 + t * 16 + 4 * (l / 16) + r, n = n0 + l % 16;
+    if (l % 16 >= NCOL || m >= g.M || n >= nout) continue;
     float o = sum[0];
     if constexpr (SILU) o = silu_bf16(round_bf16(sum[0])) * round_bf16(sum[1]);
     g.c[int64_t(m) * g.scm + n] = f32_to_bf16(o);
@@ -573,14 +576,27 @@ int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
 
 // 8 waves per block; 4 k steps of loads per wave in flight for wide outputs, 8 when N < 2048 (fewer blocks, each
 // with more of W to stream) -- the best of a sweep over 4/8/16 waves and 2/4/8 steps at the Qwen3-0.6B shapes.
-template <int MT, bool SILU>
-int launch_skinny(const MfmaArgs& g, hipStream_t s) {
+// Block tile: all rows (MT = ceil(M / 16) row tiles) x 16 columns when that gives >= 256 blocks; else one 16-row
+// tile per block (grid.y = row tiles) x 16 columns, or x 8 columns. One CU streams at most ~70 GB/s from L2/HBM,
+// and every block reads all of its rows of A (32 x K: twice the W slice of a 16-column block), so narrow outputs
+// (N = 1024: 64 blocks of 32 x 16) need the smaller tiles to reach every CU.
+template <int MT, int NCOL, bool SILU>
+int launch_skinny_tile(const MfmaArgs& g, hipStream_t s) {
   constexpr int NW = 8;
   const int nout = SILU ? g.N / 2 : g.N;
-  const dim3 grid(unsigned((nout + 15) / 16)), block(NW * 64);
-  if (g.N >= 2048) hipLaunchKernelGGL((gemm_skinny<MT, NW, 4, SILU>), grid, block, 0, s, g);
-  else hipLaunchKernelGGL((gemm_skinny<MT, NW, 8, SILU>), grid, block, 0, s, g);
+  const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((g.M + 16 * MT - 1) / (16 * MT))), block(NW * 64);
+  if (g.N >= 2048) hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 4, SILU>), grid, block, 0, s, g);
+  else hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 8, SILU>), grid, block, 0, s, g);
   return check_launch("matmul");
+}
+
+template <int MT, bool SILU>
+int launch_skinny(const MfmaArgs& g, hipStream_t s) {
+  constexpr int64_t kBlocks = 256;
+  const int64_t nout = SILU ? g.N / 2 : g.N;
+  if ((nout + 15) / 16 >= kBlocks) return launch_skinny_tile<MT, 16, SILU>(g, s);
+  if (MT > 1 && MT * ((nout + 15) / 16) >= kBlocks) return launch_skinny_tile<1, 16, SILU>(g, s);
+  return launch_skinny_tile<1, 8, SILU>(g, s);
 }
 
 template <bool SILU>
