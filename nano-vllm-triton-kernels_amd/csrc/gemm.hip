@@ -574,8 +574,8 @@ int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   }
 }
 
-// 8 waves per block; 4 k steps of loads per wave in flight for wide outputs, 8 when N < 2048 (fewer blocks, each
-// with more of W to stream) -- the best of a sweep over 4/8/16 waves and 2/4/8 steps at the Qwen3-0.6B shapes.
+// 8 waves per block; 4 k steps of loads per wave in flight for wide outputs and 8-column blocks, 8 for 16-column
+// blocks when N < 2048 -- the best of sweeps over 4/8/12/16 waves and 2/4/8/12 steps at the Qwen3-0.6B shapes.
 // Block tile: all rows (MT = ceil(M / 16) row tiles) x 16 columns when that gives >= 256 blocks; else one 16-row
 // tile per block (grid.y = row tiles) x 16 columns, or x 8 columns. One CU streams at most ~70 GB/s from L2/HBM,
 // and every block reads all of its rows of A (32 x K: twice the W slice of a 16-column block), so narrow outputs
@@ -585,7 +585,7 @@ int launch_skinny_tile(const MfmaArgs& g, hipStream_t s) {
   constexpr int NW = 8;
   const int nout = SILU ? g.N / 2 : g.N;
   const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((g.M + 16 * MT - 1) / (16 * MT))), block(NW * 64);
-  if (g.N >= 2048) hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 4, SILU>), grid, block, 0, s, g);
+  if (g.N >= 2048 || NCOL == 8) hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 4, SILU>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 8, SILU>), grid, block, 0, s, g);
   return check_launch("matmul");
 }
