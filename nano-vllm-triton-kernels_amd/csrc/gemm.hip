@@ -345,35 +345,44 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
 // and stores bf16(silu(gate) * up) of the two rounded sums (bitwise the unfused result).
 template <int MT, int NCOL, int NW, int U, bool SILU = false>
 __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
-  constexpr int NP = SILU ? 2 : 1;  // products per block: (gate, up) or the plain one
-  static_assert(NCOL == 8 || NCOL == 16, "output columns per block");
-  __shared__ float red[NW][NP][MT][4][64];
+  constexpr int NP = SILU ? 2 : 1;              // products per block: (gate, up) or the plain one
+  constexpr int NT = NCOL >= 16 ? NCOL / 16 : 1;  // 16-column MFMA tiles per block (they share the A fragments)
+  static_assert(NCOL == 8 || NCOL == 16 || NCOL == 32 || NCOL == 64, "output columns per block");
+  __shared__ float red[NW][NP][NT][MT][4][64];
   const int n0 = blockIdx.x * NCOL, m0 = blockIdx.y * 16 * MT;
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int fr = lane % 16, fk = (lane / 16) * 8;
   const int nout = SILU ? g.N / 2 : g.N;
   // with NCOL = 8 the MFMA's columns 8..15 repeat columns 0..7 (same addresses, merged by the memory pipeline)
-  const int wn = min(n0 + fr % NCOL, nout - 1);
-  const uint16_t* wrows[NP];
-  wrows[0] = g.w + int64_t(wn) * g.swn + fk;
-  if constexpr (SILU) wrows[NP - 1] = g.w + int64_t(nout + wn) * g.swn + fk;
+  const uint16_t* wrows[NP][NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int wn = min(n0 + 16 * j + (NCOL == 8 ? fr % 8 : fr), nout - 1);
+    wrows[0][j] = g.w + int64_t(wn) * g.swn + fk;
+    if constexpr (SILU) wrows[NP - 1][j] = g.w + int64_t(nout + wn) * g.swn + fk;
+  }
   const uint16_t* arow[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) arow[t] = g.a + int64_t(min(m0 + t * 16 + fr, g.M - 1)) * g.sam + fk;
-  f32x4_t acc[NP][MT];
+  f32x4_t acc[NP][NT][MT];
 #pragma unroll
   for (int p = 0; p < NP; ++p)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[p][t] = f32x4_t{};
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[p][j][t] = f32x4_t{};
   const int nks = (g.K + 31) / 32;
   for (int s0 = wave; s0 < nks; s0 += NW * U) {
-    bf16x8_t wf[U][NP], af[U][MT];
+    bf16x8_t wf[U][NP][NT], af[U][MT];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int ks = s0 + u * NW, k = ks * 32;
       const bool in = ks < nks && k + fk < g.K;  // K % 8 == 0: a lane's 8 values are all in or all out
 #pragma unroll
-      for (int p = 0; p < NP; ++p) wf[u][p] = in ? *reinterpret_cast<const bf16x8_t*>(wrows[p] + k) : bf16x8_t{};
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          wf[u][p][j] = in ? *reinterpret_cast<const bf16x8_t*>(wrows[p][j] + k) : bf16x8_t{};
 #pragma unroll
       for (int t = 0; t < MT; ++t) af[u][t] = in ? *reinterpret_cast<const bf16x8_t*>(arow[t] + k) : bf16x8_t{};
     }
@@ -382,28 +391,32 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
 #pragma unroll
       for (int p = 0; p < NP; ++p)
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-          acc[p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[u][t], wf[u][p], acc[p][t], 0, 0, 0);
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+            acc[p][j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[u][t], wf[u][p][j], acc[p][j][t], 0, 0, 0);
   }
-  // lane l, register r of tile t holds C row t*16 + 4*(l/16) + r, column n0 + l%16
+  // lane l, register r of tile (j, t) holds C row m0 + t*16 + 4*(l/16) + r, column n0 + 16 j + l%16
 #pragma unroll
   for (int p = 0; p < NP; ++p)
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][p][t][r][lane] = acc[p][t][r];
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][p][j][t][r][lane] = acc[p][j][t][r];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < MT * 256; idx += NW * 64) {
-    const int t = idx / 256, r = (idx / 64) % 4, l = idx % 64;
+  for (int idx = threadIdx.x; idx < NT * MT * 256; idx += NW * 64) {
+    const int j = idx / (MT * 256), t = (idx / 256) % MT, r = (idx / 64) % 4, l = idx % 64;
     float sum[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       sum[p] = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) sum[p] += red[w][p][t][r][l];
+      for (int w = 0; w < NW; ++w) sum[p] += red[w][p][j][t][r][l];
     }
-    const int m = m0 + t * 16 + 4 * (l / 16) + r, n = n0 + l % 16;
-    if (l % 16 >= NCOL || m >= g.M || n >= nout) continue;
+    const int m = m0 + t * 16 + 4 * (l / 16) + r, n = n0 + 16 * j + l % 16;
+    if ((NCOL == 8 && l % 16 >= 8) || m >= g.M || n >= nout) continue;
     float o = sum[0];
     if constexpr (SILU) o = silu_bf16(round_bf16(sum[0])) * round_bf16(sum[1]);
     g.c[int64_t(m) * g.scm + n] = f32_to_bf16(o);
@@ -594,6 +607,9 @@ template <int MT, bool SILU>
 int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   constexpr int64_t kBlocks = 256;
   const int64_t nout = SILU ? g.N / 2 : g.N;
+  // very wide outputs (the LM head): 64 columns per block, so each block's A reads serve four times the W bytes
+  if constexpr (!SILU)
+    if ((nout + 63) / 64 >= 8 * kBlocks) return launch_skinny_tile<MT, 64, SILU>(g, s);
   if ((nout + 15) / 16 >= kBlocks) return launch_skinny_tile<MT, 16, SILU>(g, s);
   if (MT > 1 && MT * ((nout + 15) / 16) >= kBlocks) return launch_skinny_tile<1, 16, SILU>(g, s);
   return launch_skinny_tile<1, 8, SILU>(g, s);

@@ -80,6 +80,19 @@ def test_qwen_projection_shapes(layer, M):
     torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("M", [1, 17, 32])
+def test_decode_tiles_wide_and_narrow_outputs(M):
+    """M <= 32 picks its block tile by the output width: 64 columns for an LM-head-wide output (151 936 = the Qwen3
+    vocabulary, not a multiple of 64), one 16-row tile x 8 columns for N = 1024, and the ragged tails of both."""
+    for N, K in [(151936, 1024), (1024, 3072), (1000, 72)]:
+        g = torch.Generator("cpu").manual_seed(M * 7 + N + K)
+        a = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+        w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+        c = matmul(a, w.t())
+        ref = oracle.matmul_fp64(a.cpu(), w.cpu().t())
+        torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
+
+
 def test_fp32_4096_cube():
     g = torch.Generator("cpu").manual_seed(4096)
     a = torch.randn(4096, 4096, generator=g).to(DEV)
