@@ -101,6 +101,23 @@ int nvhip_matmul_silu_mul_bf16(void* out, const void* a, const void* w, int64_t 
                                int64_t sam, int64_t swn, int64_t som, void* stream);
 
 /*
+ * RMSNorm (or Add+RMSNorm) of the rows of x fused into the projection that follows it, for decode batches
+ * (1 <= M <= 32): out = matmul(norm, W^T), or with silu != 0 the SiLU x Mul epilogue of
+ * nvhip_matmul_silu_mul_bf16 (W = [Wg; Wu] of shape [2N, K]), where norm = RMSNorm(x + residual) and
+ * residual_out = bf16(x + residual) -- or norm = RMSNorm(x) when residual is null. One launch, bitwise
+ * nvhip_add_rms_norm_bf16 / nvhip_rms_norm_bf16 followed by nvhip_matmul / nvhip_matmul_silu_mul_bf16.
+ * Not in the reference's kernels: the norm that precedes a projection in models/qwen3.py:166-183
+ * (input_layernorm -> qkv_proj, post_attention_layernorm -> gate_up_proj) moved into the projection.
+ *   x [M, K] row stride sx; residual [M, K] row stride sr, or null (then residual_out is null too);
+ *   residual_out [M, K] contiguous, not overlapping x or residual (every block reads them); norm_w [K];
+ *   W [N or 2N, K] row stride swn; out [M, N] row stride som. K = 1024 or 2048; 16-byte aligned, K-contiguous
+ *   rows; row strides multiples of 8. Anything else is rejected (NVHIP_EINVAL): run the two launches.
+ */
+int nvhip_rms_norm_matmul_bf16(void* out, void* residual_out, const void* x, const void* residual,
+                               const void* norm_w, float eps, const void* w, int64_t M, int64_t N, int64_t K,
+                               int64_t sx, int64_t sr, int64_t swn, int64_t som, int silu, void* stream);
+
+/*
  * Paged KV-cache write (unfused).
  * Replaces store_kvcache() of nanovllm/layers/attention.py:34-41 (its Triton kernel :11-31).
  *   key, value: n rows of row_elems elements (Hkv * head_dim) at ptr + t*stride (elements contiguous).

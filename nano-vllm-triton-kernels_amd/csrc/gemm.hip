@@ -424,6 +424,156 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------------------
+// RMSNorm (or Add+RMSNorm) of the A rows fused into the decode GEMM (M <= 32): the norm that precedes a projection
+// (input_layernorm -> qkv, post_attention_layernorm -> gate_up) in the same launch. Every block normalises the
+// 16 * MT rows it multiplies -- K = 64 * VPL * 8, 64 lanes per row, each lane the same VPL 16-byte vectors and the
+// same fp32 order as norm_kernel<64, VPL, ADD> (rms_norm.hip), so the normalised bf16 values are bitwise that
+// kernel's output -- into LDS, and the blocks of the first column tile also write the residual sum. The block's
+// W fragments (one round: K / 32 k steps over NW waves x U) are loaded before the norm, so the norm's loads and
+// reduction run under them; the A fragments then come from LDS. The per-column k order is that of gemm_skinny, so
+// the product is bitwise the two-launch result (norm, then matmul / matmul_silu_mul).
+struct NormMfmaArgs {
+  MfmaArgs g;              // g.a is not used: A = norm(x [+ r])
+  const uint16_t* x;       // [M, K], row stride sx
+  const uint16_t* r;       // residual [M, K], row stride sr (ADD)
+  const uint16_t* nw;      // norm weight [K]
+  uint16_t* res_out;       // [M, K] contiguous: bf16(x + r) (ADD)
+  int64_t sx, sr;
+  float inv_n, eps;
+};
+
+template <int MT, int NCOL, bool SILU, int VPL, bool ADD>
+__global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
+  constexpr int NW = 8;
+  constexpr int K = 64 * VPL * 8, KP = K + 8;  // LDS row pitch: the 16 rows of a fragment read hit distinct banks
+  constexpr int U = K / 32 / NW;               // k steps per wave: the whole K in one round
+  constexpr int R = 16 * MT;                   // rows of this block
+  constexpr int NP = SILU ? 2 : 1;
+  constexpr int NT = NCOL >= 16 ? NCOL / 16 : 1;
+  static_assert(NCOL == 8 || NCOL == 16, "output columns per block");
+  static_assert(U >= 1 && U * 32 * NW == K, "one round of k steps");
+  __shared__ __attribute__((aligned(16))) uint16_t As[R * KP];
+  __shared__ float red[NW][NP][NT][MT][4][64];
+  const MfmaArgs& g = a.g;
+  const int n0 = blockIdx.x * NCOL, m0 = blockIdx.y * R;
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int fr = lane % 16, fk = (lane / 16) * 8;
+  const int nout = SILU ? g.N / 2 : g.N;
+
+  // W fragments of the whole K (wave w: k steps w, w + NW, ...), issued first
+  bf16x8_t wf[U][NP][NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int wn = min(n0 + 16 * j + (NCOL == 8 ? fr % 8 : fr), nout - 1);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint16_t* wrow = g.w + int64_t(p == 0 ? wn : nout + wn) * g.swn + fk;
+#pragma unroll
+      for (int u = 0; u < U; ++u) wf[u][p][j] = *reinterpret_cast<const bf16x8_t*>(wrow + (wave + u * NW) * 32);
+    }
+  }
+
+  // the block's rows, normalised, into LDS (wave w: rows w, w + NW, ...; rows past M are zero)
+#pragma unroll
+  for (int i = 0; i < R / NW; ++i) {
+    const int rl = wave + i * NW, m = m0 + rl;
+    uint16_t* dst = As + rl * KP;
+    if (m >= g.M) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(dst + (j * 64 + lane) * 8) = u32x4{0, 0, 0, 0};
+      continue;
+    }
+    const uint16_t* xr = a.x + int64_t(m) * a.sx;
+    float v[VPL][8];
+    u32x4 raw[VPL], wraw[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) raw[j] = load8<true>(xr + (j * 64 + lane) * 8);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) wraw[j] = load8<true>(a.nw + (j * 64 + lane) * 8);
+    if constexpr (ADD) {
+      const uint16_t* rr = a.r + int64_t(m) * a.sr;
+      u32x4 rraw[VPL];
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) rraw[j] = load8<true>(rr + (j * 64 + lane) * 8);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        float xf[8], rf[8];
+        unpack8(raw[j], xf);
+        unpack8(rraw[j], rf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = xf[e] + rf[e];
+        if (blockIdx.x == 0) store8<true>(a.res_out + int64_t(m) * K + (j * 64 + lane) * 8, pack8(v[j]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) unpack8(raw[j], v[j]);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+    ss = group_sum<64>(ss);
+    const float rstd = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float wfl[8], o[8];
+      unpack8(wraw[j], wfl);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = round_bf16(v[j][e] * rstd) * wfl[e];
+      *reinterpret_cast<u32x4*>(dst + (j * 64 + lane) * 8) = pack8(o);
+    }
+  }
+  __syncthreads();
+
+  f32x4_t acc[NP][NT][MT];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[p][j][t] = f32x4_t{};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int k = (wave + u * NW) * 32;
+    bf16x8_t af[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) af[t] = *reinterpret_cast<const bf16x8_t*>(As + (t * 16 + fr) * KP + k + fk);
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          acc[p][j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], wf[u][p][j], acc[p][j][t], 0, 0, 0);
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][p][j][t][r][lane] = acc[p][j][t][r];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < NT * MT * 256; idx += NW * 64) {
+    const int j = idx / (MT * 256), t = (idx / 256) % MT, r = (idx / 64) % 4, l = idx % 64;
+    float sum[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      sum[p] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum[p] += red[w][p][j][t][r][l];
+    }
+    const int m = m0 + t * 16 + 4 * (l / 16) + r, n = n0 + 16 * j + l % 16;
+    if ((NCOL == 8 && l % 16 >= 8) || m >= g.M || n >= nout) continue;
+    float o = sum[0];
+    if constexpr (SILU) o = silu_bf16(round_bf16(sum[0])) * round_bf16(sum[1]);
+    g.c[int64_t(m) * g.scm + n] = f32_to_bf16(o);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
 // fp32 MFMA kernel: v_mfma_f32_32x32x2_f32 forms exact fp32 products and accumulates them in fp32 (precision
 // "ieee"); with TF32 every input is first rounded to tf32. A is K-contiguous; B is either K-contiguous (W [N, K],
 // B = W.t()) or N-contiguous ([K, N]). 128x128 block tile, 4 waves of 64x64 (2x2 MFMA tiles, operands swapped as
@@ -615,6 +765,25 @@ int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   return launch_skinny_tile<1, 8, SILU>(g, s);
 }
 
+template <int MT, int NCOL, bool SILU, int VPL, bool ADD>
+int launch_skinny_norm_tile(const NormMfmaArgs& a, hipStream_t s) {
+  const int nout = SILU ? a.g.N / 2 : a.g.N;
+  const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((a.g.M + 16 * MT - 1) / (16 * MT))), block(512);
+  hipLaunchKernelGGL((gemm_skinny_norm<MT, NCOL, SILU, VPL, ADD>), grid, block, 0, s, a);
+  return check_launch("rms_norm_matmul");
+}
+
+// The block tiles of launch_skinny (without the 64-column one); K = 2048 keeps one 16-row tile per block so that
+// the normalised rows (16 x 2056 bf16) and the reduction buffer fit the LDS.
+template <bool SILU, int VPL, bool ADD>
+int launch_skinny_norm(const NormMfmaArgs& a, hipStream_t s) {
+  const int64_t nout = SILU ? a.g.N / 2 : a.g.N, cols16 = (nout + 15) / 16;
+  if constexpr (VPL == 2)
+    if (a.g.M > 16 && cols16 >= 256) return launch_skinny_norm_tile<2, 16, SILU, VPL, ADD>(a, s);
+  if (cols16 * ((a.g.M + 15) / 16) >= 256) return launch_skinny_norm_tile<1, 16, SILU, VPL, ADD>(a, s);
+  return launch_skinny_norm_tile<1, 8, SILU, VPL, ADD>(a, s);
+}
+
 template <bool SILU>
 int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   if (g.M <= 16) return launch_skinny<1, SILU>(g, s);
@@ -701,4 +870,52 @@ extern "C" int nvhip_matmul_silu_mul_bf16(void* out, const void* a, const void* 
   MfmaArgs m{static_cast<uint16_t*>(out), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(w),
              int(M), int(2 * N2), int(K), sam, swn, som};
   return launch_mfma_auto<true>(m, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nvhip_rms_norm_matmul_bf16(void* out, void* residual_out, const void* x, const void* residual,
+                                          const void* norm_w, float eps, const void* w, int64_t M, int64_t N,
+                                          int64_t K, int64_t sx, int64_t sr, int64_t swn, int64_t som, int silu,
+                                          void* stream) {
+  using namespace nvhip;
+  clear_error();
+  if (M < 0 || N < 0) return invalid("rms_norm_matmul: negative size");
+  if (M > 32) return invalid("rms_norm_matmul: at most 32 rows (decode batches)");
+  if (K != 1024 && K != 2048) return invalid("rms_norm_matmul: K (the norm width) must be 1024 or 2048");
+  if (M == 0 || N == 0) return NVHIP_OK;
+  const bool add = residual != nullptr;
+  if (!out || !x || !norm_w || !w || (add && !residual_out) || (!add && residual_out))
+    return invalid("rms_norm_matmul: null pointer (residual_out is given exactly when residual is)");
+  if (sx < K || swn < K || som < N || (add && sr < K) || sx % 8 || swn % 8 || (add && sr % 8))
+    return invalid("rms_norm_matmul: bad strides (K-contiguous rows, row strides multiples of 8)");
+  if (!aligned16(x) || !aligned16(norm_w) || !aligned16(w) || (add && (!aligned16(residual) || !aligned16(residual_out))))
+    return invalid("rms_norm_matmul: x, residual, residual_out, norm_w and w must be 16-byte aligned");
+  if (add) {  // residual_out is read by no block, but x and residual are read by every block: no overlap
+    const auto* ro = static_cast<const char*>(residual_out);
+    const auto overlaps = [&](const void* p, int64_t stride) {
+      const auto* b = static_cast<const char*>(p);
+      return ro < b + ((M - 1) * stride + K) * 2 && b < ro + M * K * 2;
+    };
+    if (overlaps(x, sx) || overlaps(residual, sr))
+      return invalid("rms_norm_matmul: residual_out must not overlap x or residual");
+  }
+  if (N >= (int64_t(1) << 30)) return invalid("rms_norm_matmul: N too large");
+  NormMfmaArgs a{};
+  a.g = MfmaArgs{static_cast<uint16_t*>(out), nullptr, static_cast<const uint16_t*>(w), int(M),
+                 int(silu ? 2 * N : N), int(K), 0, swn, som};
+  a.x = static_cast<const uint16_t*>(x);
+  a.r = static_cast<const uint16_t*>(residual);
+  a.nw = static_cast<const uint16_t*>(norm_w);
+  a.res_out = static_cast<uint16_t*>(residual_out);
+  a.sx = sx, a.sr = sr, a.inv_n = 1.0f / float(K), a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define NVHIP_NORM_MM(SI, V, AD) return launch_skinny_norm<SI, V, AD>(a, s)
+  if (K == 1024) {
+    if (silu) { if (add) NVHIP_NORM_MM(true, 2, true); NVHIP_NORM_MM(true, 2, false); }
+    if (add) NVHIP_NORM_MM(false, 2, true);
+    NVHIP_NORM_MM(false, 2, false);
+  }
+  if (silu) { if (add) NVHIP_NORM_MM(true, 4, true); NVHIP_NORM_MM(true, 4, false); }
+  if (add) NVHIP_NORM_MM(false, 4, true);
+  NVHIP_NORM_MM(false, 4, false);
+#undef NVHIP_NORM_MM
 }

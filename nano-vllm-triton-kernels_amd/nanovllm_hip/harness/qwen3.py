@@ -9,9 +9,11 @@ backend "hip"   : rms_norm / fused_add_rms_norm_ (residual in place) / silu_and_
 backend "torch" : the layers' own torch code run eagerly (what the reference's "compile" backend compiles), with
                   the unfused q_norm, k_norm, rotary and KV scatter.
 The projections and the tied LM head use the HIP GEMM (nanovllm_hip.kernels.matmul, the wiring of linear.py:51,
-:73, :153 and embed_head.py:63; gate_up with the SiLU x Mul epilogue, matmul_silu_and_mul) in the hip backend and
-torch's F.linear in the torch backend; forward(..., linear="torch") makes the hip backend use F.linear and the
-separate silu_and_mul, so that token differences come only from the four kernels.
+:73, :153 and embed_head.py:63; gate_up with the SiLU x Mul epilogue) in the hip backend, with the norm before the
+qkv and gate_up projections inside those GEMMs for decode batches (rms_norm_matmul / add_rms_norm_matmul, bitwise
+the separate launches), and torch's F.linear in the torch backend; forward(..., linear="torch") makes the hip
+backend use F.linear, the separate norms and the separate silu_and_mul, so that token differences come only from
+the four kernels.
 Both backends share the embedding and the attention. The attention is chosen apart
 from the backend: "torch" = the fp32 code below (prefill and decode), "hip" = the HIP paged decode attention
 (nanovllm_hip.kernels.attention, the flash_attn_with_kvcache call of layers/attention.py:84-90) for decode steps,
@@ -182,18 +184,28 @@ class Qwen3:
         hq, hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         h = F.embedding(input_ids, self.embed)
         residual = None
+        # hip backend with the HIP GEMM: each norm runs inside the projection that follows it (one launch; bitwise
+        # the norm then the GEMM) for decode batches, and as the two launches for longer inputs
+        fuse = backend == "hip" and linear == "hip"
         for li, L in enumerate(self.layers):
             k_cache, v_cache = self.kv[li]
-            # input_layernorm
-            if residual is None:
-                residual = h
-                h = hip.rms_norm(h, L["input_norm"], eps) if backend == "hip" else rms_forward(h, L["input_norm"], eps)
-            elif backend == "hip":
-                h, residual = hip.fused_add_rms_norm_(h, residual, L["input_norm"], eps)
+            # input_layernorm + qkv projection; q/k/v are strided views of the projection output
+            if fuse:
+                if residual is None:
+                    residual = h
+                    qkv = hip.rms_norm_matmul(h, L["input_norm"], eps, L["qkv"])
+                else:
+                    qkv, residual = hip.add_rms_norm_matmul(h, residual, L["input_norm"], eps, L["qkv"])
             else:
-                h, residual = add_rms_forward(h, residual, L["input_norm"], eps)
-            # attention pre-segment: q/k/v are strided views of the qkv projection output
-            qkv = lin(h, L["qkv"])
+                if residual is None:
+                    residual = h
+                    h = hip.rms_norm(h, L["input_norm"], eps) if backend == "hip" else \
+                        rms_forward(h, L["input_norm"], eps)
+                elif backend == "hip":
+                    h, residual = hip.fused_add_rms_norm_(h, residual, L["input_norm"], eps)
+                else:
+                    h, residual = add_rms_forward(h, residual, L["input_norm"], eps)
+                qkv = lin(h, L["qkv"])
             q, k, v = qkv.split([hq * D, hkv * D, hkv * D], dim=-1)
             q, k, v = q.view(-1, hq, D), k.view(-1, hkv, D), v.view(-1, hkv, D)
             if backend == "hip":
@@ -221,12 +233,11 @@ class Qwen3:
                 o = paged_decode_attention(q, k_cache, v_cache, ctx.block_tables, ctx.context_lens, self.scale)
             h = lin(o.reshape(o.shape[0], hq * D), L["o"])
             # post_attention_layernorm + MLP
-            if backend == "hip":
+            if fuse:   # norm, gate_up projection and SiLU x Mul in one launch (bitwise the three-step result)
+                h, residual = hip.add_rms_norm_matmul(h, residual, L["post_norm"], eps, L["gate_up"], silu=True)
+            elif backend == "hip":
                 h, residual = hip.fused_add_rms_norm_(h, residual, L["post_norm"], eps)
-                if linear == "hip":   # gate_up projection and SiLU x Mul in one launch (bitwise the two-step result)
-                    h = hip.matmul_silu_and_mul(h, L["gate_up"])
-                else:
-                    h = hip.silu_and_mul(lin(h, L["gate_up"]))
+                h = hip.silu_and_mul(lin(h, L["gate_up"]))
             else:
                 h, residual = add_rms_forward(h, residual, L["post_norm"], eps)
                 gate, up = F.linear(h, L["gate_up"]).chunk(2, -1)

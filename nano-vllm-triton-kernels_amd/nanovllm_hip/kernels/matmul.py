@@ -30,3 +30,40 @@ def matmul_silu_and_mul(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.
         from nanovllm_hip.kernels.swiglu import silu_and_mul
         return silu_and_mul(matmul(x, gate_up_weight.t()))
     return torch.ops.nvhip.matmul_silu_mul(x, gate_up_weight)
+
+
+def _fusable(x, residual, norm_w, weight):
+    M, K = x.shape
+    tensors = [x, norm_w, weight] + ([residual] if residual is not None else [])
+    return (1 <= M <= 32 and K in (1024, 2048) and x.dtype == norm_w.dtype == weight.dtype == torch.bfloat16
+            and all(t.stride(-1) == 1 and t.data_ptr() % 16 == 0 for t in tensors)
+            and all(t.stride(0) % 8 == 0 for t in tensors if t.dim() == 2))
+
+
+def rms_norm_matmul(x: torch.Tensor, norm_w: torch.Tensor, eps: float, weight: torch.Tensor,
+                    silu: bool = False) -> torch.Tensor:
+    """matmul(rms_norm(x, norm_w, eps), weight.t()) -- or matmul_silu_and_mul of it when silu -- in one launch for
+    decode batches (x [M, K] with M <= 32, K = 1024 or 2048); weight [N, K] ([2 * I, K] with silu). Bitwise the
+    two-launch result, which it falls back to for other shapes (the norm that precedes a projection,
+    models/qwen3.py:166-183, moved into it)."""
+    assert x.ndim == 2 and weight.ndim == 2 and x.shape[1] == weight.shape[1] and norm_w.shape == (x.shape[1],)
+    if not _fusable(x, None, norm_w, weight):
+        from nanovllm_hip.kernels.rms_norm import rms_norm
+        h = rms_norm(x, norm_w, eps)
+        return matmul_silu_and_mul(h, weight) if silu else matmul(h, weight.t())
+    out, _ = torch.ops.nvhip.rms_norm_matmul(x, None, norm_w, float(eps), weight, silu)
+    return out
+
+
+def add_rms_norm_matmul(x: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                        weight: torch.Tensor, silu: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """(matmul(RMSNorm(x + residual), weight.t()), x + residual) -- the product as matmul_silu_and_mul when silu --
+    in one launch for decode batches (M <= 32, K = 1024 or 2048); the new residual is a new tensor. Bitwise
+    fused_add_rms_norm followed by matmul / matmul_silu_and_mul, which it falls back to for other shapes."""
+    assert x.ndim == 2 and x.shape == residual.shape and weight.ndim == 2 and x.shape[1] == weight.shape[1]
+    assert norm_w.shape == (x.shape[1],)
+    if not _fusable(x, residual, norm_w, weight):
+        from nanovllm_hip.kernels.rms_norm import fused_add_rms_norm
+        h, res = fused_add_rms_norm(x, residual, norm_w, eps)
+        return (matmul_silu_and_mul(h, weight) if silu else matmul(h, weight.t())), res
+    return torch.ops.nvhip.rms_norm_matmul(x, residual, norm_w, float(eps), weight, silu)

@@ -23,6 +23,8 @@ _DEF.define("fused_add_rms_norm_(Tensor x, Tensor(a!) residual, Tensor w, float 
 _DEF.define("silu_and_mul(Tensor x) -> Tensor")
 _DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
 _DEF.define("matmul_silu_mul(Tensor a, Tensor w) -> Tensor")
+_DEF.define("rms_norm_matmul(Tensor x, Tensor? residual, Tensor norm_w, float eps, Tensor w, bool silu) "
+            "-> (Tensor, Tensor)")
 _DEF.define("prefill_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
             "int max_seqlen_q, float scale, bool causal, Tensor? block_table) -> Tensor")
 _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
@@ -229,6 +231,32 @@ _DEF.impl("matmul_silu_mul", _matmul_silu_mul_impl, "CUDA")
 @torch.library.register_fake("nvhip::matmul_silu_mul")
 def _matmul_silu_mul_fake(a, w):
     return torch.empty((a.shape[0], w.shape[0] // 2), dtype=a.dtype, device=a.device)
+
+
+# ------------------------------------------------------------------ RMSNorm / Add+RMSNorm fused into the next GEMM
+
+def _rms_norm_matmul_impl(x, residual, norm_w, eps, w, silu):
+    M, K = x.shape
+    N = w.shape[0] // 2 if silu else w.shape[0]
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    res_out = torch.empty_like(x, memory_format=torch.contiguous_format) if residual is not None else x.new_empty((0,))
+    status = _lib.lib().nvhip_rms_norm_matmul_bf16(
+        out.data_ptr(), res_out.data_ptr() if residual is not None else None, x.data_ptr(),
+        residual.data_ptr() if residual is not None else None, norm_w.data_ptr(), eps, w.data_ptr(), M, N, K,
+        x.stride(0), residual.stride(0) if residual is not None else 0, w.stride(0), out.stride(0),
+        int(silu), _lib.stream_of(x))
+    _lib.check(status, "rms_norm_matmul")
+    return out, res_out
+
+
+_DEF.impl("rms_norm_matmul", _rms_norm_matmul_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::rms_norm_matmul")
+def _rms_norm_matmul_fake(x, residual, norm_w, eps, w, silu):
+    N = w.shape[0] // 2 if silu else w.shape[0]
+    out = torch.empty((x.shape[0], N), dtype=x.dtype, device=x.device)
+    return out, (torch.empty_like(x) if residual is not None else x.new_empty((0,)))
 
 
 # ------------------------------------------------------------------ prefill (varlen) attention

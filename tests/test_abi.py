@@ -135,3 +135,22 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
     assert fm(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 4, 8, 12, 16, 16, 8, P) == \
         _lib.NVHIP_EINVAL and "K % 8" in _err()
     assert fm(P, P, P, 0, 8, 16, 16, 16, 8, P) == _lib.NVHIP_OK
+
+
+def test_rms_norm_matmul_rejects_bad_arguments_without_launching():
+    f = _lib.lib().nvhip_rms_norm_matmul_bf16
+    A = ctypes.c_void_p(1 << 20)   # 16-byte aligned stand-ins: every call below returns before touching them
+    B = ctypes.c_void_p(2 << 20)
+
+    def call(M=32, N=4096, K=1024, res=A, res_out=B, x=ctypes.c_void_p(3 << 20), sx=1024, silu=0):
+        return f(ctypes.c_void_p(4 << 20), res_out, x, res, ctypes.c_void_p(5 << 20), 1e-6,
+                 ctypes.c_void_p(6 << 20), M, N, K, sx, 1024, 1024, N, silu, None)
+
+    assert call(M=33) == _lib.NVHIP_EINVAL and "32 rows" in _err()
+    assert call(K=1000) == _lib.NVHIP_EINVAL and "1024 or 2048" in _err()
+    assert call(res_out=None) == _lib.NVHIP_EINVAL and "residual_out" in _err()
+    assert call(res=None) == _lib.NVHIP_EINVAL and "residual_out" in _err()     # residual_out without residual
+    assert call(sx=1000) == _lib.NVHIP_EINVAL and "strides" in _err()
+    assert call(x=ctypes.c_void_p((3 << 20) + 8)) == _lib.NVHIP_EINVAL and "aligned" in _err()
+    assert call(res_out=ctypes.c_void_p((1 << 20) + 2048 * 16)) == _lib.NVHIP_EINVAL and "overlap" in _err()
+    assert call(M=0) == _lib.NVHIP_OK and _err() == ""
