@@ -323,6 +323,44 @@ def e2e_decode_step(torch, dev, batch=32, layers=28, min_len=512, max_len=2048, 
     return out
 
 
+def e2e_mixed_step(torch, dev, decodes=16, chunk=240, layers=28, min_len=512, max_len=2048, reps=20):
+    """One mixed step of the same model: `decodes` decode requests (prompts of U[512, 2048] random ids, prefilled
+    first) and a `chunk`-token prefill chunk, 256 tokens in all, through the hip backend with the HIP varlen paged
+    attention. Timed as piecewise HIP graphs (one per segment between two attentions, the attentions eager) and
+    as the same segments run eagerly: microseconds per step."""
+    from nanovllm_hip.harness.decode import Batch, prefill
+    from nanovllm_hip.harness.mixed import Piecewise, Request, prepare_mixed
+    from nanovllm_hip.harness.qwen3 import Qwen3, Qwen3Config
+    cfg = Qwen3Config(num_hidden_layers=layers)
+    model = Qwen3(cfg, dev, seed=0)
+    b = Batch(cfg, decodes, 4, min_len, max_len, 0, dev)
+    model.allocate_kv_cache(b.num_blocks + 1)
+    first, _ = prefill(model, b, "hip")
+    reqs = [Request(p.tolist() + [t], tab, len(p)) for p, tab, t in zip(b.prompts, b.tables, first)]
+    g = torch.Generator().manual_seed(5)
+    reqs.append(Request(torch.randint(0, cfg.vocab_size, (chunk,), generator=g).tolist(), [b.num_blocks], 0, chunk))
+    ids, pos, ctx, _ = prepare_mixed(reqs, 256, dev)
+    n = ids.shape[0]
+    out = {"tokens": n, "decode_requests": decodes, "prefill_chunk": chunk, "layers": layers}
+    for name, pw in (("eager_us", Piecewise(model, [n])), ("piecewise_graph_us", Piecewise(model, [n]))):
+        if name == "piecewise_graph_us":
+            pw.record()
+        for _ in range(3):
+            pw.run(ids, pos, ctx)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            pw.run(ids, pos, ctx)
+        end.record()
+        end.synchronize()
+        out[name] = round(start.elapsed_time(end) * 1e3 / reps, 1)
+        del pw
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_ceiling(torch, dev, mib=1024, reps=20):
     """Device copy (torch copy_) of `mib` MiB: the practical read+write bandwidth ceiling, in GB/s."""
     n = mib * 2 ** 20 // 2
@@ -442,6 +480,7 @@ def main():
         result["extra"]["copy_ceiling_GB/s"] = copy_ceiling(torch, dev)
         if not args.no_e2e:
             result["extra"]["e2e_decode_step"] = e2e_decode_step(torch, dev)
+            result["extra"]["e2e_mixed_step"] = e2e_mixed_step(torch, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, oracle, T)
     print(json.dumps(result), flush=True)

@@ -46,11 +46,19 @@ class Qwen3Config:
 
 @dataclass
 class Context:
-    """Per-forward batch layout (the fields of nano-vllm's utils/context.py this model reads)."""
+    """Per-forward batch layout (the fields of nano-vllm's utils/context.py this model reads).
+
+    Prefill without block_tables: one sequence, its own keys. Prefill with block_tables (a mixed step or a prefix
+    cache, model_runner.py:489-496): varlen over the paged cache, sequence s has queries cu_seqlens_q[s] ..
+    cu_seqlens_q[s+1] and keys 0 .. cu_seqlens_k[s+1] - cu_seqlens_k[s] (this step's KV is stored first)."""
     is_prefill: bool
     slot_mapping: torch.Tensor          # [T] int32, -1 = no KV write
     context_lens: torch.Tensor | None = None   # decode: [B] int32
-    block_tables: torch.Tensor | None = None   # decode: [B, max_blocks] int32 (padded with 0)
+    block_tables: torch.Tensor | None = None   # decode / varlen prefill: [B, max_blocks] int32 (padded with 0)
+    cu_seqlens_q: torch.Tensor | None = None   # varlen prefill: [B + 1] int32
+    cu_seqlens_k: torch.Tensor | None = None
+    max_seqlen_q: int = 0
+    max_seqlen_k: int = 0
 
 
 # ------------------------------------------------------------------ torch code of the layers (backend "torch")
@@ -133,6 +141,32 @@ def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scal
     return o.reshape(B, hq, d).to(q.dtype)
 
 
+def varlen_paged_attention(q, k_cache, v_cache, block_tables, cu_seqlens_q, cu_seqlens_k, scale):
+    """Varlen causal attention over the paged cache in fp32 (the flash_attn_varlen_func call with block_table of
+    layers/attention.py:77-83): sequence s's queries are the last lq of its lk cached tokens, query i sees keys
+    0 .. lk - lq + i. Eager only (the loop reads the sequence bounds on the host)."""
+    hq, d = q.shape[1], q.shape[2]
+    bs, hkv = k_cache.shape[1], k_cache.shape[2]
+    g = hq // hkv
+    cq, ck = cu_seqlens_q.tolist(), cu_seqlens_k.tolist()
+    out = torch.empty_like(q)
+    for s in range(len(cq) - 1):
+        lq, lk = cq[s + 1] - cq[s], ck[s + 1] - ck[s]
+        nb = (lk + bs - 1) // bs
+        blocks = block_tables[s, :nb].long()
+        kk = k_cache[blocks].reshape(nb * bs, hkv, d)[:lk].float()          # [lk, Hkv, D]
+        vv = v_cache[blocks].reshape(nb * bs, hkv, d)[:lk].float()
+        qf = q[cq[s]:cq[s + 1]].float().view(lq, hkv, g, d).permute(1, 2, 0, 3).contiguous()  # [Hkv, G, lq, D]
+        kt = kk.permute(1, 2, 0).contiguous().unsqueeze(1)                  # [Hkv, 1, D, lk]
+        vf = vv.permute(1, 0, 2).contiguous().unsqueeze(1)                  # [Hkv, 1, lk, D]
+        sc = torch.matmul(qf, kt) * scale                                   # [Hkv, G, lq, lk]
+        allowed = torch.arange(lk, device=q.device)[None, :] <= (lk - lq + torch.arange(lq, device=q.device))[:, None]
+        sc.masked_fill_(~allowed, float("-inf"))
+        o = torch.matmul(torch.softmax(sc, dim=-1), vf)                     # [Hkv, G, lq, D]
+        out[cq[s]:cq[s + 1]] = o.permute(2, 0, 1, 3).reshape(lq, hq, d).to(q.dtype)
+    return out
+
+
 def hip_linear(x, w):
     """nn.Linear without bias through the HIP GEMM: x [T, in] @ w[out, in]^T (B = w.t(), the K-contiguous layout)."""
     return hip.matmul(x, w.t())
@@ -163,7 +197,7 @@ class Qwen3:
                 input_norm=norm_w(H), post_norm=norm_w(H), q_norm=norm_w(D), k_norm=norm_w(D),
                 qkv=randn((hq + 2 * hkv) * D, H), o=randn(H, hq * D),
                 gate_up=randn(2 * I, H), down=randn(H, I)))
-        self.final_norm = norm_w(H)
+        self.final_norm_w = norm_w(H)
         self.cos_sin = rope_table(D, cfg.max_position_embeddings, cfg.rope_theta).to(device)
         self.kv = None  # [(k_cache, v_cache)] per layer
         self.scale = D ** -0.5
@@ -175,79 +209,107 @@ class Qwen3:
         self.kv = [(cache[0, i], cache[1, i]) for i in range(c.num_hidden_layers)]
         return cache
 
+    def pre_attn(self, li, positions, h, residual, backend, linear="hip"):
+        """Layer li up to its attention (models/qwen3.py:185-197 with Qwen3Attention.pre_attn :89-105): the input
+        norm and the qkv projection, plus the q/k norms and RoPE in the torch backend. Returns (q, k, v, residual):
+        strided [T, heads, D] views of the projection output. In the hip backend q and k are not normed or rotated
+        yet -- the fused kernel in attn() does that together with the KV write, as the reference's fused_norm_rope
+        path does. Reads nothing of the batch layout (Context), so a piecewise graph can record it."""
+        c, L = self.cfg, self.layers[li]
+        eps, hq, hkv, D = c.rms_norm_eps, c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        # hip backend with the HIP GEMM: the norm runs inside the projection that follows it (one launch, bitwise
+        # the norm then the GEMM) for decode batches, and as the two launches for longer inputs
+        if backend == "hip" and linear == "hip":
+            if residual is None:
+                residual = h
+                qkv = hip.rms_norm_matmul(h, L["input_norm"], eps, L["qkv"])
+            else:
+                qkv, residual = hip.add_rms_norm_matmul(h, residual, L["input_norm"], eps, L["qkv"])
+        else:
+            if residual is None:
+                residual = h
+                h = hip.rms_norm(h, L["input_norm"], eps) if backend == "hip" else \
+                    rms_forward(h, L["input_norm"], eps)
+            elif backend == "hip":
+                h, residual = hip.fused_add_rms_norm_(h, residual, L["input_norm"], eps)
+            else:
+                h, residual = add_rms_forward(h, residual, L["input_norm"], eps)
+            qkv = F.linear(h, L["qkv"])
+        q, k, v = qkv.split([hq * D, hkv * D, hkv * D], dim=-1)
+        q, k, v = q.view(-1, hq, D), k.view(-1, hkv, D), v.view(-1, hkv, D)
+        if backend != "hip":
+            q = rms_forward(q, L["q_norm"], eps)
+            k = rms_forward(k, L["k_norm"], eps)
+            cos, sin = self.cos_sin[positions].chunk(2, dim=-1)
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        return q, k, v, residual
+
+    def attn(self, li, q, k, v, positions, ctx: Context, backend, attention="torch"):
+        """Attention.forward of layer li (layers/attention.py:64-92): the KV write (hip: the fused q/k norm + RoPE
+        + KV-write kernel) and the attention over the batch layout in ctx -> o [T, Hq, D]."""
+        c, L = self.cfg, self.layers[li]
+        hq, D = c.num_attention_heads, c.head_dim
+        k_cache, v_cache = self.kv[li]
+        varlen = ctx.is_prefill and ctx.block_tables is not None
+        if backend == "hip":
+            write_k = ctx.is_prefill and not varlen     # only a prefill without the cache reads k from here
+            q, k_out = hip.qk_norm_rope_kv(q, k, v, positions, L["q_norm"], L["k_norm"], c.rms_norm_eps,
+                                           self.cos_sin, k_cache, v_cache, ctx.slot_mapping, write_k)
+            if write_k:
+                k = k_out
+        else:
+            store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
+        if varlen and attention == "hip":
+            return flash_attn_varlen_func(q, k_cache, v_cache, ctx.max_seqlen_q, ctx.cu_seqlens_q, ctx.max_seqlen_k,
+                                          ctx.cu_seqlens_k, self.scale, causal=True, block_table=ctx.block_tables)
+        if varlen:
+            return varlen_paged_attention(q, k_cache, v_cache, ctx.block_tables, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                          self.scale)
+        if ctx.is_prefill and attention == "hip":
+            T = q.shape[0]
+            cu = torch.tensor([0, T], dtype=torch.int32, device=q.device)
+            return flash_attn_varlen_func(q, k, v, T, cu, T, cu, self.scale, causal=True)
+        if ctx.is_prefill:
+            return prefill_attention(q, k, v, self.scale)
+        if attention == "hip":
+            B = ctx.context_lens.shape[0]
+            return flash_attn_with_kvcache(q.view(B, -1, hq, D), k_cache, v_cache, ctx.context_lens,
+                                           ctx.block_tables, self.scale, causal=True).view(-1, hq, D)
+        return paged_decode_attention(q, k_cache, v_cache, ctx.block_tables, ctx.context_lens, self.scale)
+
+    def post_attn(self, li, o, residual, backend, linear="hip"):
+        """Layer li after its attention (models/qwen3.py:199-209): o_proj, the post-attention norm and the MLP.
+        Returns (h, residual); like pre_attn it reads nothing of the batch layout."""
+        c, L = self.cfg, self.layers[li]
+        eps, hq, D = c.rms_norm_eps, c.num_attention_heads, c.head_dim
+        lin = hip_linear if backend == "hip" and linear == "hip" else F.linear
+        h = lin(o.reshape(o.shape[0], hq * D), L["o"])
+        if backend == "hip" and linear == "hip":   # norm, gate_up and SiLU x Mul in one launch for decode batches
+            h, residual = hip.add_rms_norm_matmul(h, residual, L["post_norm"], eps, L["gate_up"], silu=True)
+        elif backend == "hip":
+            h, residual = hip.fused_add_rms_norm_(h, residual, L["post_norm"], eps)
+            h = hip.silu_and_mul(lin(h, L["gate_up"]))
+        else:
+            h, residual = add_rms_forward(h, residual, L["post_norm"], eps)
+            gate, up = F.linear(h, L["gate_up"]).chunk(2, -1)
+            h = F.silu(gate) * up
+        return lin(h, L["down"]), residual
+
+    def final_norm(self, h, residual, backend):
+        """The model's last Add+RMSNorm (models/qwen3.py:232) -> hidden states [T, hidden]."""
+        if backend == "hip":
+            return hip.fused_add_rms_norm_(h, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]
+        return add_rms_forward(h, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]
+
     def forward(self, input_ids, positions, ctx: Context, backend: str, attention: str = "torch",
                 linear: str = "hip"):
         """Returns the final hidden states [T, hidden] (after the last norm)."""
-        c = self.cfg
-        lin = hip_linear if backend == "hip" and linear == "hip" else F.linear
-        eps = c.rms_norm_eps
-        hq, hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
-        h = F.embedding(input_ids, self.embed)
-        residual = None
-        # hip backend with the HIP GEMM: each norm runs inside the projection that follows it (one launch; bitwise
-        # the norm then the GEMM) for decode batches, and as the two launches for longer inputs
-        fuse = backend == "hip" and linear == "hip"
-        for li, L in enumerate(self.layers):
-            k_cache, v_cache = self.kv[li]
-            # input_layernorm + qkv projection; q/k/v are strided views of the projection output
-            if fuse:
-                if residual is None:
-                    residual = h
-                    qkv = hip.rms_norm_matmul(h, L["input_norm"], eps, L["qkv"])
-                else:
-                    qkv, residual = hip.add_rms_norm_matmul(h, residual, L["input_norm"], eps, L["qkv"])
-            else:
-                if residual is None:
-                    residual = h
-                    h = hip.rms_norm(h, L["input_norm"], eps) if backend == "hip" else \
-                        rms_forward(h, L["input_norm"], eps)
-                elif backend == "hip":
-                    h, residual = hip.fused_add_rms_norm_(h, residual, L["input_norm"], eps)
-                else:
-                    h, residual = add_rms_forward(h, residual, L["input_norm"], eps)
-                qkv = lin(h, L["qkv"])
-            q, k, v = qkv.split([hq * D, hkv * D, hkv * D], dim=-1)
-            q, k, v = q.view(-1, hq, D), k.view(-1, hkv, D), v.view(-1, hkv, D)
-            if backend == "hip":
-                q, k_out = hip.qk_norm_rope_kv(q, k, v, positions, L["q_norm"], L["k_norm"], eps, self.cos_sin,
-                                               k_cache, v_cache, ctx.slot_mapping, ctx.is_prefill)
-                if ctx.is_prefill:
-                    k = k_out
-            else:
-                q = rms_forward(q, L["q_norm"], eps)
-                k = rms_forward(k, L["k_norm"], eps)
-                cos, sin = self.cos_sin[positions].chunk(2, dim=-1)
-                q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-                store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
-            if ctx.is_prefill and attention == "hip":
-                T = q.shape[0]
-                cu = torch.tensor([0, T], dtype=torch.int32, device=q.device)
-                o = flash_attn_varlen_func(q, k, v, T, cu, T, cu, self.scale, causal=True)
-            elif ctx.is_prefill:
-                o = prefill_attention(q, k, v, self.scale)
-            elif attention == "hip":
-                B = ctx.context_lens.shape[0]
-                o = flash_attn_with_kvcache(q.view(B, -1, hq, D), k_cache, v_cache, ctx.context_lens,
-                                            ctx.block_tables, self.scale, causal=True).view(-1, hq, D)
-            else:
-                o = paged_decode_attention(q, k_cache, v_cache, ctx.block_tables, ctx.context_lens, self.scale)
-            h = lin(o.reshape(o.shape[0], hq * D), L["o"])
-            # post_attention_layernorm + MLP
-            if fuse:   # norm, gate_up projection and SiLU x Mul in one launch (bitwise the three-step result)
-                h, residual = hip.add_rms_norm_matmul(h, residual, L["post_norm"], eps, L["gate_up"], silu=True)
-            elif backend == "hip":
-                h, residual = hip.fused_add_rms_norm_(h, residual, L["post_norm"], eps)
-                h = hip.silu_and_mul(lin(h, L["gate_up"]))
-            else:
-                h, residual = add_rms_forward(h, residual, L["post_norm"], eps)
-                gate, up = F.linear(h, L["gate_up"]).chunk(2, -1)
-                h = F.silu(gate) * up
-            h = lin(h, L["down"])
-        if backend == "hip":
-            h, _ = hip.fused_add_rms_norm_(h, residual, self.final_norm, eps)
-        else:
-            h, _ = add_rms_forward(h, residual, self.final_norm, eps)
-        return h
+        h, residual = F.embedding(input_ids, self.embed), None
+        for li in range(len(self.layers)):
+            q, k, v, residual = self.pre_attn(li, positions, h, residual, backend, linear)
+            o = self.attn(li, q, k, v, positions, ctx, backend, attention)
+            h, residual = self.post_attn(li, o, residual, backend, linear)
+        return self.final_norm(h, residual, backend)
 
     def logits(self, h, fp32=False, backend="torch", linear="hip"):
         """Tied LM head (embed_head.py:56-68): bf16 like the reference (then fp32 for sampling), or with fp32=True
@@ -267,4 +329,4 @@ def num_params(cfg: Qwen3Config) -> int:
     return cfg.vocab_size * H + cfg.num_hidden_layers * per_layer + H
 
 
-__all__ = ["Qwen3Config", "Context", "Qwen3", "num_params"]
+__all__ = ["Qwen3Config", "Context", "Qwen3", "num_params", "varlen_paged_attention"]
