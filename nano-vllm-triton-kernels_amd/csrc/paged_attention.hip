@@ -30,6 +30,9 @@
 // rounded to bf16.
 // The block-table entries of the block's token range are loaded once, one per lane, alongside the context length
 // and Q.
+// Varlen: a paged prefill call (prefill_attention.hip) hands its sequences with few queries (<= 16 / G each, e.g.
+// the decode requests of a mixed step) to this kernel, with per-sequence query rows and context lengths from
+// cu_seqlens; the prefill kernel's 128-query tiles would spend a whole tile's work per key on them.
 // Small batches: with a caller workspace the context of each (sequence, kv head) is split over several blocks
 // (whole 256-token rounds) when there are fewer pairs than CUs; each block writes its merged (max, sum, O) record
 // and a second kernel merges the records in split order. Without a workspace one block covers the whole context.
@@ -63,6 +66,11 @@ struct DecodeArgs {
   int splits;     // context splits per (sequence, kv head): blocks s = 0 .. splits-1 take tokens
   int split_len;  // [s * split_len, (s + 1) * split_len); a multiple of kChunk * kWaves (so of kChunk * waves)
   float* ws;      // splits > 1: [num_seqs, Hkv, splits, RP, 2 + D] fp32 records (max, sum, O) of each block
+  // varlen (the short sequences of a paged prefill call, splits = 1): sequence b's queries are rows cu_q[b] ..
+  // cu_q[b+1]-1 of q and out and its context is cu_k[b+1] - cu_k[b] keys; a sequence with no queries or more
+  // than q_len is left alone (the prefill kernel takes it). Null: q_len queries per sequence, ctx_lens.
+  const int32_t* cu_q;
+  const int32_t* cu_k;
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -111,11 +119,19 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
   const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
   const int b = pair / g.Hkv, kvh = pair % g.Hkv;
   const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  const int rows = g.G * g.q_len;
+  int q0 = b * g.q_len, lq = g.q_len, ctx;  // the sequence's first query row, its queries and context length
+  if (g.cu_q != nullptr) {
+    q0 = g.cu_q[b];
+    lq = g.cu_q[b + 1] - q0;
+    if (lq < 1 || lq > g.q_len) return;  // the whole block: b is uniform
+    ctx = min(max(g.cu_k[b + 1] - g.cu_k[b], 0), g.max_blocks * g.bs);
+  } else {
+    ctx = min(max(g.ctx_lens[b], 0), g.max_blocks * g.bs);
+  }
+  const int rows = g.G * lq;
   const int32_t* bt_row = g.bt + int64_t(b) * g.max_blocks;
   const int tok_begin = split * g.split_len, blk0 = tok_begin / g.bs;
-  // issued together: the context length, this split's first 64 block-table entries (one per lane), the Q rows
-  const int ctx = min(max(g.ctx_lens[b], 0), g.max_blocks * g.bs);
+  // issued together: this split's first 64 block-table entries (one per lane) and the Q rows
   const int bt_lane = blk0 + lane < g.max_blocks ? bt_row[blk0 + lane] : -1;
 
   // Q rows as the MFMA B operand: lane l holds row l % 16, dims 32c + 8 (l / 16) .. +8
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
   if (qrow < rows) {
     qi = qrow / g.G;
     const int hh = qrow % g.G;
-    const uint16_t* qp = g.q + int64_t(b * g.q_len + qi) * g.q_st + int64_t(kvh * g.G + hh) * g.q_sh + q8;
+    const uint16_t* qp = g.q + int64_t(q0 + qi) * g.q_st + int64_t(kvh * g.G + hh) * g.q_sh + q8;
 #pragma unroll
     for (int c = 0; c < KC; ++c) qf[c] = load_bf16x8(qp + 32 * c);
   } else {
@@ -133,7 +149,7 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
     for (int c = 0; c < KC; ++c) qf[c] = bf16x8_t{};
   }
   // row qrow sees tokens < row_limit
-  const int row_limit = qrow >= rows ? 0 : g.causal ? min(max(ctx - g.q_len + qi + 1, 0), ctx) : ctx;
+  const int row_limit = qrow >= rows ? 0 : g.causal ? min(max(ctx - lq + qi + 1, 0), ctx) : ctx;
 
   float m_run = -INFINITY;  // reference max of row qrow (the same in the 4 lanes of the row)
   float l_run = 0.0f;       // this lane's part of the row sum
@@ -298,7 +314,7 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
     }
     const float o = den > 0.0f ? num / den : 0.0f;
     const int i = r / g.G, hh = r % g.G;
-    g.out[int64_t(b * g.q_len + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
+    g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
   }
 }
 
@@ -373,6 +389,25 @@ int64_t workspace_bytes(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv
 }
 
 }  // namespace
+
+int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                        const int32_t* block_table, const int32_t* cu_q, const int32_t* cu_k, int num_seqs, int qmax,
+                        int Hq, int Hkv, int D, int block_size, int num_blocks, int max_blocks, int64_t q_st,
+                        int64_t q_sh, int64_t o_st, int64_t o_sh, float scale, int causal, hipStream_t s) {
+  const int G = Hq / Hkv, rows = G * qmax;
+  if (qmax < 1 || rows > 16 || (D != 64 && D != 128 && D != 256) ||
+      int64_t(num_seqs) * Hkv > INT32_MAX || int64_t(max_blocks) * block_size > INT32_MAX)
+    return invalid("prefill_attention: short-sequence path: bad sizes");
+  DecodeArgs g{out, q, k_cache, v_cache, block_table, nullptr, qmax, Hkv, G, block_size, num_blocks, max_blocks,
+               q_st, q_sh, o_st, o_sh, scale * 1.4426950408889634f, causal ? 1 : 0, 1,
+               max_blocks * block_size, nullptr, cu_q, cu_k};
+  switch (D) {
+    case 64: return launch_decode_rows<64>(g, num_seqs, rows, s);
+    case 128: return launch_decode_rows<128>(g, num_seqs, rows, s);
+    default: return launch_decode_rows<256>(g, num_seqs, rows, s);
+  }
+}
+
 }  // namespace nvhip
 
 extern "C" int64_t nvhip_paged_decode_attention_workspace_size(int64_t num_seqs, int64_t q_len, int64_t Hq,
@@ -430,6 +465,8 @@ extern "C" int nvhip_paged_decode_attention_bf16(void* out, const void* q, const
                causal ? 1 : 0,
                1,
                int(max_blocks * block_size),
+               nullptr,
+               nullptr,
                nullptr};
   // split the context over several blocks when the caller gave a large enough workspace
   const int64_t need = workspace_bytes(num_seqs, q_len, Hq, Hkv, D, max_blocks * block_size);

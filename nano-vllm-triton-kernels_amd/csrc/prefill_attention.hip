@@ -58,6 +58,7 @@ struct PrefillArgs {
   float scale_log2;  // softmax scale * log2(e), > 0
   int causal;
   int qtiles, nhg;  // query tiles per sequence (from max_seqlen_q), head groups (Hq / heads per block)
+  int lq_skip;      // sequences with 1 .. lq_skip queries are left to the paged decode kernel
 };
 
 // Element offset of key j of sequence b, kv head kvh, in k (v with v_st): a contiguous row, or (PAGED) the cache
@@ -101,6 +102,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   const int h = hg * HB + int(threadIdx.x) / kHeadThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
+  if (lq >= 1 && lq <= g.lq_skip) return;  // the whole block: b is uniform
   if (qt * kBQ >= lq || lk <= 0) {
     const int r = int(threadIdx.x) % kHeadThreads;
     if (qt * kBQ < lq && r < kBQ && qt * kBQ + r < lq) {  // no keys: zero rows
@@ -393,6 +395,7 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
                 scale * 1.4426950408889634f,
                 causal ? 1 : 0,
                 0,
+                0,
                 0};
   g.qtiles = int(qtiles);
   g.nhg = int(Hq / hb);
@@ -401,6 +404,20 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kThreads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool paged = block_table != nullptr;
+  // With the cache (a mixed step, a prefix-cache chunk), sequences with at most 16 / G queries -- the decode
+  // requests of a mixed step -- run in the paged decode kernel, one block per (sequence, kv head) streaming its
+  // keys; the prefill kernel's blocks for them return at once.
+  const int64_t G = Hq / Hkv;
+  if (paged && G <= 16) {
+    g.lq_skip = int(std::min<int64_t>(16 / G, max_seqlen_q));
+    if (int rc = paged_decode_varlen(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(q),
+                                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), block_table,
+                                     cu_seqlens_q, cu_seqlens_k, int(num_seqs), g.lq_skip, int(Hq), int(Hkv), int(D),
+                                     int(block_size), int(num_blocks), int(max_blocks), q_stride_token,
+                                     q_stride_head, out_stride_token, out_stride_head, scale, causal, s))
+      return rc;
+    if (max_seqlen_q <= g.lq_skip) return NVHIP_OK;
+  }
 #define NVHIP_PREFILL_LAUNCH(DD, PG, HBV) hipLaunchKernelGGL((prefill_attention_kernel<DD, PG, HBV>), grid, block, 0, s, g)
   if (hb == 2 && D == 64 && paged) NVHIP_PREFILL_LAUNCH(64, true, 2);
   else if (hb == 2 && D == 64) NVHIP_PREFILL_LAUNCH(64, false, 2);

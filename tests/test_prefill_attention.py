@@ -5,7 +5,8 @@ inputs). The kernel rounds P to bf16 for P.V (as flash-attn does); tolerance: th
 atol 1e-2. Cases: a Qwen3-0.6B prefill batch (16 q / 8 kv heads, head_dim 128, k and v strided views of the qkv
 projection output), the prefix cache (keys through a block table of 256- and 16-slot blocks, NaN in unused slots),
 head_dim 64, GQA ratios 1 / 4 / 8, non-causal, more queries than keys (rows that see nothing are zero), an empty
-sequence, graph capture and replay.
+sequence, graph capture and replay; mixed steps over the cache, whose sequences with <= 16 / G queries run in the
+paged decode kernel (bitwise the decode attention's rows for one-query sequences).
 """
 import numpy as np
 import pytest
@@ -88,6 +89,56 @@ def test_prefix_cache_block_table(block_size):
             vc[blk, :cnt] = torch.randn(cnt, Hkv, D, generator=g).to(torch.bfloat16)
     q = torch.randn(sum(lq), Hq, D, generator=g).to(torch.bfloat16)
     check(q, kc, vc, cu(lq), cu(lk), True, bt)
+
+
+def paged_case(lq, lk, block_size, Hq=16, Hkv=8, D=128, seed=0):
+    """q [sum(lq), Hq, D] and paged caches holding lk[b] keys of sequence b through a random block table (NaN in
+    the unused slots)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    nb = sum((n + block_size - 1) // block_size for n in lk) + 3
+    kc = torch.full((nb, block_size, Hkv, D), float("nan")).to(torch.bfloat16)
+    vc = kc.clone()
+    perm = torch.randperm(nb, generator=g)
+    maxb = max(max((n + block_size - 1) // block_size for n in lk), 1)
+    bt = torch.full((len(lk), maxb), -1, dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(lk):
+        for c in range((n + block_size - 1) // block_size):
+            blk = int(perm[used]); used += 1
+            bt[b, c] = blk
+            cnt = min(n - c * block_size, block_size)
+            kc[blk, :cnt] = torch.randn(cnt, Hkv, D, generator=g).to(torch.bfloat16)
+            vc[blk, :cnt] = torch.randn(cnt, Hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(sum(lq), Hq, D, generator=g).to(torch.bfloat16)
+    return q, kc, vc, bt
+
+
+@pytest.mark.parametrize("block_size", [256, 16])
+def test_mixed_step_short_sequences(block_size):
+    """A mixed step: decode requests (1 query), short runs of 2 .. 9 queries and prefill chunks over the cache.
+    Sequences with <= 16 / G queries (8 here) take the paged decode kernel, the rest the prefill kernel; an
+    empty sequence and one with no cached keys are in the batch too."""
+    lq = [1, 1, 40, 1, 3, 8, 9, 1, 0, 130, 2]
+    lk = [700, 1, 300, 1500, 90, 8, 1000, 257, 0, 130, 0]
+    q, kc, vc, bt = paged_case(lq, lk, block_size, seed=block_size + 1)
+    out, _ = check(q, kc, vc, cu(lq), cu(lk), True, bt)
+    assert torch.all(out[-2:] == 0)     # the last sequence has no keys
+
+
+def test_decode_only_varlen_equals_decode_attention():
+    """Every sequence with one query: the varlen call runs only the paged decode kernel, whose rows are bitwise
+    those of flash_attn_with_kvcache on the same sequences (32 sequences x 8 kv heads: the decode call does not
+    split the contexts either)."""
+    from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
+    g = torch.Generator("cpu").manual_seed(12)
+    lk = torch.randint(1, 2049, (32,), generator=g).tolist()
+    lq = [1] * len(lk)
+    q, kc, vc, bt = paged_case(lq, lk, 256, seed=11)
+    out, _ = check(q, kc, vc, cu(lq), cu(lk), True, bt)
+    dec = flash_attn_with_kvcache(q.to(DEV).view(len(lk), 1, 16, 128), kc.to(DEV), vc.to(DEV),
+                                  torch.tensor(lk, dtype=torch.int32, device=DEV), bt.to(DEV), 128 ** -0.5,
+                                  causal=True)
+    assert torch.equal(out, dec.view(-1, 16, 128).cpu())
 
 
 def test_head_dim_64_and_gqa():
