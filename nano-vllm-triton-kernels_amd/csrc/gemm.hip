@@ -113,7 +113,8 @@ __global__ __launch_bounds__(kBlock) void gemm_generic(const GemmArgs g) {
 //
 // Data path per k-tile of 64:
 //   global -> VGPRs   16-byte loads, RS tiles in flight in registers (RS = 2 keeps 48-96 KB per block in flight,
-//                     enough to cover the ~2000-cycle L2 latency measured at full load)
+//                     enough to cover the ~2000-cycle L2 latency measured at full load; 64x64 tiles, which run
+//                     when there are few of them, use RS = 4)
 //   VGPRs -> LDS      two LDS stages, [rows][64] bf16 per operand; 16-byte chunk c of row r stored at chunk
 //                     c ^ ((r >> 1) & 7): with gfx950's 64 four-byte banks the 16 rows a half-wave fragment read
 //                     touches land in 16 distinct 16-byte bank groups (conflict-free)
@@ -156,6 +157,15 @@ __device__ __forceinline__ void tile_coords(int pid, int M, int N, int BM, int B
   pid_n = (pid % in_group) / group_rows;
 }
 
+// step(kt + S, slot S) for S = 0 .. RS - 1: the k-tiles of one pass over the RS register slots.
+template <int S, int RS, typename F>
+__device__ __forceinline__ void unroll_steps(F& step, int kt) {
+  if constexpr (S < RS) {
+    step(kt + S, std::integral_constant<int, S>{});
+    unroll_steps<S + 1, RS>(step, kt);
+  }
+}
+
 // SILU: W is [2 * N2, K] = [gate; up] (N = 2 * N2) and C is [M, N2] = bf16(silu(A Wg^T)) * bf16(A Wu^T) rounded
 // to bf16: a tile's first BN / 2 B rows are gate rows n0 / 2 .., the last BN / 2 the matching up rows N2 + n0 / 2 ..
 // (so the per-column k order is that of the plain product, and the result is bitwise the unfused one).
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   static_assert(FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
   constexpr int AC = BM * 8 / NT, BC = BN * 8 / NT, CH = AC + BC;  // 16-byte chunks per thread per k-tile
   static_assert(AC >= 1 && BC >= 1 && AC * NT == BM * 8 && BC * NT == BN * 8, "tile too small for the block");
-  static_assert(RS == 1 || RS == 2, "register stages");
+  static_assert(RS >= 1 && RS <= 8, "register stages");
   constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
   constexpr int OUT_PITCH = BN + 8;
   constexpr int LDS_ELEMS = (2 * STAGE > BM * OUT_PITCH) ? 2 * STAGE : BM * OUT_PITCH;
@@ -274,10 +284,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
       }
     }
   };
-  for (int kt = 0; kt < nk; kt += RS) {
-    step(kt, std::integral_constant<int, 0>{});
-    if constexpr (RS == 2) step(kt + 1, std::integral_constant<int, 1>{});  // nk % RS == 0 (checked on the host)
-  }
+  for (int kt = 0; kt < nk; kt += RS) unroll_steps<0, RS>(step, kt);  // nk % RS == 0 (checked on the host)
   __syncthreads();
 
   // epilogue: accumulators -> bf16 tile in LDS -> coalesced 16-byte row stores
@@ -714,13 +721,23 @@ int launch_mfma(const MfmaArgs& g, hipStream_t s) {
 // Tile shape by a cost model fitted on MI355X at the Qwen3-0.6B projections: a launch runs in ceil(tiles / 256)
 // rounds of one tile per CU, so its time goes as rounds x tile area / efficiency, the efficiency of a tile growing
 // with its size (fewer L2 bytes per flop). At M = 2048 this picks 128x256 for N = 4096, 256x192 for N = 6144 and
-// 64x128 for N = 1024 -- 256 tiles each, the fastest of a sweep over eleven shapes. 64x64 tiles for 32 < M <= 64.
+// 64x128 for N = 1024 -- 256 tiles each, the fastest of a sweep over eleven shapes.
+// When 64x64 tiles fit in one round (M <= 64, or mixed steps and prefill chunks of up to a few hundred rows) a
+// block's time is its chain of K / 64 k-tiles, each waiting on its loads: 64x64 tiles with 4 k-tiles of loads in
+// flight (RS = 4) instead of 2 (M = 256: down 22.6 -> 15.8 us, o_proj 15.4 -> 11.0, qkv 9.9 -> 7.4; deeper
+// staging measured no faster, and none of it helps once every CU has a large tile). The k order of every tile
+// shape is the same, so the result does not depend on the choice.
 template <int RS, bool KTAIL, bool SILU>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
-  if (g.M <= 64) return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU>(g, s);
+  constexpr int kCUs = 256;
+  const int64_t tiles64 = int64_t((g.M + 63) / 64) * ((g.N + 63) / 64);
+  if (g.M <= 64 || tiles64 <= kCUs) {
+    if constexpr (!KTAIL)
+      if (((g.K / kBK) & 3) == 0) return launch_mfma<64, 64, 2, 2, 4, false, SILU>(g, s);
+    return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU>(g, s);
+  }
   struct Shape { int bm, bn; double eff; };
   constexpr Shape shapes[] = {{256, 256, 1.0}, {256, 192, 1.0}, {128, 256, 0.95}, {128, 128, 0.85}, {64, 128, 0.75}};
-  constexpr int kCUs = 256;
   int best = 0;
   double best_cost = 0.0;
   for (int i = 0; i < 5; ++i) {

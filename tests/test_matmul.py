@@ -6,8 +6,8 @@ The reference's tests/test_kernels_matmul.py: torch.testing.assert_close(C, A.do
   bf16:        rtol 1.6e-2, atol 1e-2 * sqrt(K)
 over its shape grid (M = 1 decode rows, sizes that are not multiples of any tile, K < one K-tile) for B row-major
 and B = W.t() of an nn.Linear weight, plus the guard that "ieee" is not silently tf32. Added: the Qwen3-0.6B
-projection shapes at M = 32 and 2048 (bf16, B = W.t(), A ~N(0,1)/sqrt(K)), fp32 4096^3, strided/offset views and
-the committed golden products.
+projection shapes at M = 32, 256 and 2048 (bf16, B = W.t(), A ~N(0,1)/sqrt(K)), rows independent of the tile
+shape M selects, fp32 4096^3, strided/offset views and the committed golden products.
 """
 import math
 import os
@@ -67,7 +67,7 @@ def test_ieee_is_not_tf32():
 QWEN_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}
 
 
-@pytest.mark.parametrize("M", [32, 2048])
+@pytest.mark.parametrize("M", [32, 256, 2048])
 @pytest.mark.parametrize("layer", list(QWEN_SHAPES))
 def test_qwen_projection_shapes(layer, M):
     K, N = QWEN_SHAPES[layer]
@@ -78,6 +78,21 @@ def test_qwen_projection_shapes(layer, M):
     ref = oracle.matmul_fp64(a.cpu(), w.cpu().t())
     # |C| ~ 1 here (A is scaled by 1/sqrt(K)): the bf16 tolerance with atol 1e-2
     torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("layer", list(QWEN_SHAPES))
+def test_rows_do_not_depend_on_the_tile_choice(layer):
+    """Above 64 rows every MFMA tile shape (64x64 with 4 k-tiles of loads in flight while 64x64 tiles fit one round
+    on the CUs, the cost model's larger tiles beyond) sums each output in the same k order, so a row of C has the
+    same bits whatever M selects: rows of products with 100, 256 and 512 rows equal those rows of the 2048-row
+    product."""
+    K, N = QWEN_SHAPES[layer]
+    g = torch.Generator("cpu").manual_seed(K + N)
+    a = (torch.randn(2048, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    full = matmul(a, w.t())
+    for M in (100, 256, 512):
+        assert torch.equal(matmul(a[:M], w.t()), full[:M]), M
 
 
 @pytest.mark.parametrize("M", [1, 17, 32])
