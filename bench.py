@@ -17,11 +17,13 @@ T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNo
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
 the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s; the causal
 prefill attention of one layer over 4 sequences of 2048 tokens, in TFLOP/s; the end-to-end decode step of a
-random-init Qwen3-0.6B-shaped model (batch 32, HIP graph: us per step, tokens/s, kernel nodes).
+random-init Qwen3-0.6B-shaped model (batch 32, HIP graph: us per step, tokens/s, kernel nodes); a 256-token mixed
+step of the same model (16 decode requests + a 240-token prefill chunk), eager and from piecewise graphs.
 The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
 sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 8192] [--no-cpu] [--no-extra] [--no-e2e]
+       (profiling modes: --profile, --profile-gemm, --profile-e2e, --profile-prefill, --profile-mixed)
 """
 import argparse
 import json
@@ -427,6 +429,10 @@ def main():
     p.add_argument("--profile-prefill", action="store_true",
                    help="for rocprofv3 kernel traces: --steps eager launches of the prefill attention (4 x 2048 "
                         "tokens, one Qwen3-0.6B layer)")
+    p.add_argument("--profile-mixed", action="store_true",
+                   help="for rocprofv3 kernel traces: build the model, prefill 16 requests, then time the 256-token "
+                        "mixed step (16 decodes + a 240-token chunk) --steps times eagerly and --steps times from "
+                        "piecewise graphs, and print the mixed-step line")
     p.add_argument("--profile", action="store_true",
                    help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
                         "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
@@ -448,6 +454,9 @@ def main():
         return
     if args.profile_prefill:
         prefill_attention(torch, dev, args.steps, torch.Generator().manual_seed(0), profile=True)
+        return
+    if args.profile_mixed:
+        print(json.dumps(e2e_mixed_step(torch, dev, reps=args.steps)), flush=True)
         return
     if args.profile_e2e:
         print(json.dumps(e2e_decode_step(torch, dev, profile_replays=args.steps)), flush=True)
