@@ -583,11 +583,15 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
 // ------------------------------------------------------------------------------------------------------------
 // fp32 MFMA kernel: v_mfma_f32_32x32x2_f32 forms exact fp32 products and accumulates them in fp32 (precision
 // "ieee"); with TF32 every input is first rounded to tf32. A is K-contiguous; B is either K-contiguous (W [N, K],
-// B = W.t()) or N-contiguous ([K, N]). 128x128 block tile, 4 waves of 64x64 (2x2 MFMA tiles, operands swapped as
-// in the bf16 kernel), k-tile 32. LDS holds both operands k-major ([k][m], [k][n]) with a row pitch of 160
-// floats, so the two half-waves of a fragment read (rows k and k+1, 32 consecutive floats each) hit disjoint bank
-// halves. Global loads are 16 bytes: 4 consecutive k of one row of A / W (8 lanes cover one row's 128 bytes), or
-// 4 consecutive n of one row of B. The next k-tile is loaded into registers while the current one is multiplied.
+// B = W.t()) or N-contiguous ([K, N]). BM x BN block tile of WAVES_M x WAVES_N waves, each owning (BM / WAVES_M) x
+// (BN / WAVES_N) outputs as 32x32 MFMA tiles (operands swapped as in the bf16 kernel), k-tile 32. LDS holds both
+// operands k-major ([k][m], [k][n]) with row pitches of BM + 32 and BN + 32 floats (32 mod 64 banks), so the two
+// half-waves of a fragment read (rows k and k+1, 32 consecutive floats each) hit disjoint bank halves. Global loads
+// are 16 bytes: 4 consecutive k of one row of A / W (8 lanes cover one row's 128 bytes), or 4 consecutive n of one
+// row of B. The next k-tile is loaded into registers at the start of the current one and stored into the other LDS
+// stage halfway through its MFMAs (stores after the last MFMA left the matrix cores idle during them). 4096^3:
+// 256x256 tiles with 16 waves (4 per SIMD) 1107 us, 128x128 with 8 waves 1167 us, 128x128 with 4 waves and the
+// stores at the end 1434 us.
 struct F32Args {
   float* c;
   const float* a;
@@ -596,30 +600,37 @@ struct F32Args {
   int64_t sam, sbk, sbn, scm;
 };
 
-template <bool B_NMAJOR, bool TF32>
-__global__ __launch_bounds__(256) void gemm_mfma_f32(const F32Args g) {
-  constexpr int BM = 128, BN = 128, BK = 32, P = 160, NT = 256;
-  constexpr int CH = BM * BK / 4 / NT;  // 16-byte chunks per thread per operand per k-tile (4)
-  __shared__ __attribute__((aligned(16))) float lds[2][2][BK * P];  // [stage][A | B][k * P + m]
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool B_NMAJOR, bool TF32>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_f32(const F32Args g) {
+  constexpr int NT = 64 * WAVES_M * WAVES_N, BK = 32, PA = BM + 32, PB = BN + 32;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
+  constexpr int CHA = BM * BK / 4 / NT, CHB = BN * BK / 4 / NT;  // 16-byte chunks per thread per k-tile
+  static_assert(FM >= 1 && FN >= 1 && CHA >= 1 && CHB >= 1 && CHA * NT * 4 == BM * BK && CHB * NT * 4 == BN * BK,
+                "tile shape");
+  __shared__ __attribute__((aligned(16))) float lds[2][BK * (PA + PB)];  // [stage][A k-major | B k-major]
   int pid_m, pid_n;
   tile_coords(blockIdx.x, g.M, g.N, BM, BN, pid_m, pid_n);
   const int m0 = pid_m * BM, n0 = pid_n * BN;
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const int wm = wave / 2, wn = wave % 2;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // K-major chunks (A, and B when K-contiguous): chunk c covers row c / 8, k = 4 * (c % 8) .. +4
-  const float* asrc[CH];
-  const float* bsrc[CH];
-  int arow[CH], akc[CH], brow[CH], bkc[CH];
+  const float* asrc[CHA];
+  const float* bsrc[CHB];
+  int arow[CHA], akc[CHA], brow[CHB], bkc[CHB];
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
+  for (int i = 0; i < CHA; ++i) {
     const int c = tid + NT * i;
     arow[i] = c / 8;
     akc[i] = 4 * (c % 8);
     asrc[i] = g.a + int64_t(min(m0 + arow[i], g.M - 1)) * g.sam + akc[i];
-    if constexpr (B_NMAJOR) {  // chunk c covers k row c / 32, n = 4 * (c % 32) .. +4 (clamped inside N)
-      brow[i] = c / 32;
-      bkc[i] = 4 * (c % 32);
+  }
+#pragma unroll
+  for (int i = 0; i < CHB; ++i) {
+    const int c = tid + NT * i;
+    if constexpr (B_NMAJOR) {  // chunk c covers k row c / (BN / 4), n = 4 * (c % (BN / 4)) .. +4 (clamped inside N)
+      brow[i] = c / (BN / 4);
+      bkc[i] = 4 * (c % (BN / 4));
       bsrc[i] = g.b + min(n0 + bkc[i], g.N - 4);
     } else {
       brow[i] = c / 8;
@@ -627,11 +638,13 @@ __global__ __launch_bounds__(256) void gemm_mfma_f32(const F32Args g) {
       bsrc[i] = g.b + int64_t(min(n0 + brow[i], g.N - 1)) * g.sbn + bkc[i];
     }
   }
-  f32x4_t ra[CH], rb[CH];
+  f32x4_t ra[CHA], rb[CHB];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
+    for (int i = 0; i < CHA; ++i)
       ra[i] = (k0 + akc[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(asrc[i] + k0) : f32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < CHB; ++i) {
       if constexpr (B_NMAJOR)
         rb[i] = (k0 + brow[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(bsrc[i] + int64_t(k0 + brow[i]) * g.sbk)
                                      : f32x4_t{0, 0, 0, 0};
@@ -641,27 +654,29 @@ __global__ __launch_bounds__(256) void gemm_mfma_f32(const F32Args g) {
   };
   auto tf = [](float x) { return TF32 ? round_tf32(x) : x; };
   auto lstore = [&](int st) {
-    float* la = lds[st][0];
-    float* lb = lds[st][1];
+    float* la = lds[st];
+    float* lb = lds[st] + BK * PA;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
+    for (int i = 0; i < CHA; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) la[(akc[i] + e) * P + arow[i]] = tf(ra[i][e]);
+      for (int e = 0; e < 4; ++e) la[(akc[i] + e) * PA + arow[i]] = tf(ra[i][e]);
+#pragma unroll
+    for (int i = 0; i < CHB; ++i) {
       if constexpr (B_NMAJOR) {
-        *reinterpret_cast<f32x4_t*>(&lb[brow[i] * P + bkc[i]]) =
+        *reinterpret_cast<f32x4_t*>(&lb[brow[i] * PB + bkc[i]]) =
             f32x4_t{tf(rb[i][0]), tf(rb[i][1]), tf(rb[i][2]), tf(rb[i][3])};
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) lb[(bkc[i] + e) * P + brow[i]] = tf(rb[i][e]);
+        for (int e = 0; e < 4; ++e) lb[(bkc[i] + e) * PB + brow[i]] = tf(rb[i][e]);
       }
     }
   };
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16_t{};
   const int fr = lane % 32, fk = lane / 32;
   const int nk = (g.K + BK - 1) / BK;
   gload(0);
@@ -670,35 +685,34 @@ __global__ __launch_bounds__(256) void gemm_mfma_f32(const F32Args g) {
   for (int kt = 0; kt < nk; ++kt) {
     const bool more = kt + 1 < nk;
     if (more) gload((kt + 1) * BK);
-    const float* la = lds[kt & 1][0];
-    const float* lb = lds[kt & 1][1];
+    const float* la = lds[kt & 1];
+    const float* lb = lds[kt & 1] + BK * PA;
 #pragma unroll
     for (int kp = 0; kp < BK / 2; ++kp) {
-      const int row = (2 * kp + fk) * P;
-      float af[2], bfv[2];
+      float af[FM], bfv[FN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = la[row + wm * 64 + i * 32 + fr];
+      for (int i = 0; i < FM; ++i) af[i] = la[(2 * kp + fk) * PA + wm * WM + i * 32 + fr];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bfv[j] = lb[row + wn * 64 + j * 32 + fr];
+      for (int j = 0; j < FN; ++j) bfv[j] = lb[(2 * kp + fk) * PB + wn * WN + j * 32 + fr];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bfv[j], af[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bfv[j], af[i], acc[i][j], 0, 0, 0);
+      if (kp == BK / 4 - 1 && more) lstore((kt + 1) & 1);  // the other stage: nobody reads it during this k-tile
     }
-    if (more) lstore((kt + 1) & 1);
     __syncthreads();
   }
-  // lane holds C row m0 + wm*64 + i*32 + lane%32, columns n0 + wn*64 + j*32 + 8*q + 4*(lane/32) .. +4
+  // lane holds C row m0 + wm*WM + i*32 + lane%32, columns n0 + wn*WN + j*32 + 8*q + 4*(lane/32) .. +4
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int m = m0 + wm * 64 + i * 32 + fr;
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WM + i * 32 + fr;
     if (m >= g.M) continue;
     float* crow = g.c + int64_t(m) * g.scm;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * fk;
+        const int n = n0 + wn * WN + j * 32 + 8 * q + 4 * fk;
         const f32x4_t v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
         if (n + 4 <= g.N && (reinterpret_cast<uintptr_t>(crow + n) & 15) == 0) {
           *reinterpret_cast<f32x4_t*>(crow + n) = v;
@@ -811,11 +825,20 @@ int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   return launch_mfma_shape<1, false, SILU>(g, s);
 }
 
+// 256x256 tiles (16 waves) when they fill the CUs at least once, else 128x128 (8 waves). The 256x256 kernel with
+// tf32 rounding of an N-major B needs more than the 128 VGPRs a 1024-thread block leaves a lane: 128x128 there.
 template <bool B_NMAJOR, bool TF32>
 int launch_f32(const F32Args& g, hipStream_t s) {
+  const int64_t big = int64_t((g.M + 255) / 256) * ((g.N + 255) / 256);
+  if (big >= 256 && !(B_NMAJOR && TF32)) {
+    if (big > INT32_MAX) return invalid("matmul: matrix too large");
+    if constexpr (!(B_NMAJOR && TF32))
+      hipLaunchKernelGGL((gemm_mfma_f32<256, 256, 4, 4, B_NMAJOR, TF32>), dim3(unsigned(big)), dim3(1024), 0, s, g);
+    return check_launch("matmul");
+  }
   const int64_t tiles = int64_t((g.M + 127) / 128) * ((g.N + 127) / 128);
   if (tiles > INT32_MAX) return invalid("matmul: matrix too large");
-  hipLaunchKernelGGL((gemm_mfma_f32<B_NMAJOR, TF32>), dim3(unsigned(tiles)), dim3(256), 0, s, g);
+  hipLaunchKernelGGL((gemm_mfma_f32<128, 128, 2, 4, B_NMAJOR, TF32>), dim3(unsigned(tiles)), dim3(512), 0, s, g);
   return check_launch("matmul");
 }
 
