@@ -480,9 +480,24 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
     }
   }
 
-  // the block's rows, normalised, into LDS (wave w: rows w, w + NW, ...; rows past M are zero)
+  // the block's rows, normalised, into LDS (wave w: rows w, w + NW, ...; rows past M are zero). All of the wave's
+  // row loads are issued before the first store: the new-residual stores could alias the next rows' inputs for
+  // all the compiler knows, so loads written after them would have to wait for them.
+  constexpr int RW = R / NW;  // rows per wave
+  u32x4 raw[RW][VPL], rraw[RW][VPL], wraw[VPL];
 #pragma unroll
-  for (int i = 0; i < R / NW; ++i) {
+  for (int i = 0; i < RW; ++i) {
+    const int m = min(m0 + wave + i * NW, g.M - 1);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) raw[i][j] = load8<true>(a.x + int64_t(m) * a.sx + (j * 64 + lane) * 8);
+    if constexpr (ADD)
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) rraw[i][j] = load8<true>(a.r + int64_t(m) * a.sr + (j * 64 + lane) * 8);
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) wraw[j] = load8<true>(a.nw + (j * 64 + lane) * 8);
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
     const int rl = wave + i * NW, m = m0 + rl;
     uint16_t* dst = As + rl * KP;
     if (m >= g.M) {
@@ -490,30 +505,20 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
       for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(dst + (j * 64 + lane) * 8) = u32x4{0, 0, 0, 0};
       continue;
     }
-    const uint16_t* xr = a.x + int64_t(m) * a.sx;
     float v[VPL][8];
-    u32x4 raw[VPL], wraw[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) raw[j] = load8<true>(xr + (j * 64 + lane) * 8);
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) wraw[j] = load8<true>(a.nw + (j * 64 + lane) * 8);
     if constexpr (ADD) {
-      const uint16_t* rr = a.r + int64_t(m) * a.sr;
-      u32x4 rraw[VPL];
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) rraw[j] = load8<true>(rr + (j * 64 + lane) * 8);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         float xf[8], rf[8];
-        unpack8(raw[j], xf);
-        unpack8(rraw[j], rf);
+        unpack8(raw[i][j], xf);
+        unpack8(rraw[i][j], rf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[j][e] = xf[e] + rf[e];
         if (blockIdx.x == 0) store8<true>(a.res_out + int64_t(m) * K + (j * 64 + lane) * 8, pack8(v[j]));
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) unpack8(raw[j], v[j]);
+      for (int j = 0; j < VPL; ++j) unpack8(raw[i][j], v[j]);
     }
     float ss = 0.0f;
 #pragma unroll
