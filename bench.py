@@ -439,8 +439,9 @@ def main():
                         "byte counters; prints the launch list instead of the JSON line")
     args = p.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the kernel path has no collective; "
-              "see the sharding notes in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print(f"bench.py: --gpus {args.gpus}: only one GPU is measured (the kernel path has no collective: under "
+              "tensor parallelism each rank runs these kernels on its own head / column shard). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
