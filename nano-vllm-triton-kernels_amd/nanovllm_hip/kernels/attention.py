@@ -1,8 +1,9 @@
 """Attention over the paged KV cache: the HIP replacements of the two flash-attn calls in nano-vllm's layers.
 
 flash_attn_varlen_func (prefill, nanovllm/layers/attention.py:77-83): variable-length causal attention over the
-new tokens' own k, v, or -- with a block table, the prefix cache -- over the paged caches. Kernel:
-csrc/prefill_attention.hip.
+new tokens' own k, v, or -- with a block table (the prefix cache, a mixed prefill + decode step) -- over the paged
+caches. Kernel: csrc/prefill_attention.hip; with a block table, the sequences that bring at most 16 / (Hq / Hkv)
+queries (a mixed step's decode requests) run inside the same call in the paged decode kernel.
 
 flash_attn_with_kvcache (decode):
 
