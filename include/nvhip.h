@@ -156,22 +156,38 @@ int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_ca
  * Variable-length (prefill) attention.
  * Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale,
  * causal, block_table) as called at nanovllm/layers/attention.py:77-83 (prefill branch).
- *   q, out: [Tq, Hq, D] bf16 (token / head strides in elements, rows of D contiguous); sequence b owns tokens
+ *   q, out: [total_q, Hq, D] bf16 (token / head strides in elements, rows of D contiguous); sequence b owns tokens
  *   cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1 (int32 [num_seqs + 1]); max_seqlen_q bounds their count.
- *   Keys of sequence b: lk = cu_seqlens_k[b+1] - cu_seqlens_k[b]. Without a block table, key j is row
- *   cu_seqlens_k[b] + j of k, v [Tk, Hkv, D] (token strides k_stride_token, v_stride_token). With a block table
- *   ([num_seqs, max_blocks] int32, prefix cache), k and v are the paged caches [num_blocks, block_size, Hkv, D] and
- *   key j is slot block_table[b][j / block_size] * block_size + j % block_size (invalid blocks are skipped).
+ *   Keys of sequence b: lk = cu_seqlens_k[b+1] - cu_seqlens_k[b] (max_seqlen_k bounds it). Without a block table,
+ *   key j is row cu_seqlens_k[b] + j of k, v [Tk, Hkv, D] (token strides k_stride_token, v_stride_token). With a
+ *   block table ([num_seqs, max_blocks] int32, prefix cache / mixed steps), k and v are the paged caches
+ *   [num_blocks, block_size, Hkv, D] and key j is slot block_table[b][j / block_size] * block_size + j % block_size
+ *   (invalid blocks are skipped); then sequences with at most 16 / (Hq / Hkv) queries (decode requests of a mixed
+ *   step) are computed by the paged decode kernel inside this call.
  *   Query i of a sequence with lq queries sees keys j <= lk - lq + i when causal, all lk otherwise; a query that
  *   sees no key gets zeros. Head h reads kv head h / (Hq / Hkv). D: 64, 128.
+ *   workspace: device memory of at least nvhip_prefill_attention_workspace_size(...) bytes, 16-byte aligned
+ *   (contents need no initialisation), or NULL / too small: then the keys of a sequence are never split over
+ *   blocks. With it, few query tiles over long key ranges (a prompt chunk over its cached prefix) are spread over
+ *   the CUs in key ranges whose partial results a second kernel merges. Calls that share a workspace must be
+ *   ordered on one stream.
  * Numerics: fp32 scores and online softmax, P rounded to bf16 for P.V (as flash-attn), fp32 accumulation, bf16 out.
  */
 int nvhip_prefill_attention_bf16(void* out, const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
-                                 const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t max_seqlen_q, int64_t Hq,
-                                 int64_t Hkv, int64_t D, int64_t q_stride_token, int64_t q_stride_head,
-                                 int64_t k_stride_token, int64_t v_stride_token, int64_t out_stride_token,
-                                 int64_t out_stride_head, const int32_t* block_table, int64_t block_size,
-                                 int64_t num_blocks, int64_t max_blocks, float scale, int causal, void* stream);
+                                 const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t max_seqlen_q,
+                                 int64_t max_seqlen_k, int64_t total_q, int64_t Hq, int64_t Hkv, int64_t D,
+                                 int64_t q_stride_token, int64_t q_stride_head, int64_t k_stride_token,
+                                 int64_t v_stride_token, int64_t out_stride_token, int64_t out_stride_head,
+                                 const int32_t* block_table, int64_t block_size, int64_t num_blocks,
+                                 int64_t max_blocks, float scale, int causal, void* workspace,
+                                 int64_t workspace_size, void* stream);
+
+/*
+ * Bytes of workspace nvhip_prefill_attention_bf16 uses for these sizes (0: it does not split). Host-only, no GPU
+ * work. An addition of this library (flash-attn allocates its own split buffers).
+ */
+int64_t nvhip_prefill_attention_workspace_size(int64_t num_seqs, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                               int64_t Hq, int64_t Hkv, int64_t D, int64_t total_q);
 
 /*
  * Bytes of workspace nvhip_paged_decode_attention_bf16 uses for these sizes (0: it does not split). Host-only, no

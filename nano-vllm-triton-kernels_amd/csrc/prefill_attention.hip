@@ -27,6 +27,10 @@
 // twice the flops.
 // P is rounded to bf16 for the P.V product (as flash-attn does) and the row sum adds the fp32 p (as flash-attn
 // does); scores, softmax and O are fp32; output bf16. The softmax scale must be positive.
+// Key splits (with a caller workspace): when the blocks of one pass leave CUs idle and the key ranges are long (a
+// prompt chunk over its cached prefix: 2 query tiles x 8 head pairs = 16 blocks streaming thousands of keys each),
+// each (query tile, sequence, head group) is cut into key ranges run by separate blocks; each writes its queries'
+// (max, sum, O) records and prefill_combine merges them in split order.
 #include <algorithm>
 
 #include "common.h"
@@ -59,7 +63,15 @@ struct PrefillArgs {
   int causal;
   int qtiles, nhg;  // query tiles per sequence (from max_seqlen_q), head groups (Hq / heads per block)
   int lq_skip;      // sequences with 1 .. lq_skip queries are left to the paged decode kernel
+  int splits;       // key ranges per (query tile, sequence, head group): split s takes keys s * split_len ..
+  int split_len;    // a multiple of kBK
+  int Hq;
+  int64_t ws_rows;  // Tq: query rows of one split's records
+  float* ws;        // splits > 1: [splits, Tq, Hq, D + 4] fp32 records (max, sum, -, -, O) merged by prefill_combine
 };
+
+// fp32 elements of one (split, query, head) record: max, row sum, two unused (16-byte aligned O), O[D].
+__host__ __device__ constexpr int record_len(int D) { return D + 4; }
 
 // Element offset of key j of sequence b, kv head kvh, in k (v with v_st): a contiguous row, or (PAGED) the cache
 // slot of block blk (-1 if the block is not valid).
@@ -88,26 +100,43 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // heaviest query tile (most keys) first across its groups, so that no long tile starts late (longest-first list
   // scheduling; starting one group's tiles before the next group's left a third of the CUs idle at the end of a
   // 4 x 2048-token prefill). Otherwise all groups' tiles are dealt heaviest first.
-  const int nblk = gridDim.x, ngrp = nblk / g.qtiles;
-  int grp, qt;
-  if (nblk % 8 == 0 && (nblk / 8) % g.qtiles == 0) {
-    const int gx = nblk / 8 / g.qtiles, r = blockIdx.x / 8;
+  // With key splits, the (query tile, split) pairs of a group are its tiles, heaviest (latest query tile, first
+  // split) first.
+  const int ntile = g.qtiles * g.splits;
+  const int nblk = gridDim.x, ngrp = nblk / ntile;
+  int grp, ci;
+  if (nblk % 8 == 0 && (nblk / 8) % ntile == 0) {
+    const int gx = nblk / 8 / ntile, r = blockIdx.x / 8;
     grp = (blockIdx.x % 8) * gx + r % gx;
-    qt = g.qtiles - 1 - r / gx;
+    ci = r / gx;
   } else {
     grp = blockIdx.x % ngrp;
-    qt = g.qtiles - 1 - blockIdx.x / ngrp;
+    ci = blockIdx.x / ngrp;
   }
+  const int qt = g.qtiles - 1 - ci / g.splits, split = ci % g.splits;
   const int b = grp / g.nhg, hg = grp % g.nhg;
   const int h = hg * HB + int(threadIdx.x) / kHeadThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
   if (lq >= 1 && lq <= g.lq_skip) return;  // the whole block: b is uniform
-  if (qt * kBQ >= lq || lk <= 0) {
+  // keys [k_beg, k_stop) of this block: the split's range, cut at the last key its query tile sees
+  const int k_beg = split * g.split_len;
+  const int k_hi = split == g.splits - 1 ? INT32_MAX : k_beg + g.split_len;  // the last split takes the rest
+  const int k_stop = g.causal ? min(min(lk, lk - lq + min(qt * kBQ + kBQ, lq)), k_hi) : min(lk, k_hi);
+  if (qt * kBQ >= lq || k_stop <= k_beg) {
+    // no keys for this block: zero rows (one pass), or records that say so (the merge then writes zeros)
     const int r = int(threadIdx.x) % kHeadThreads;
-    if (qt * kBQ < lq && r < kBQ && qt * kBQ + r < lq) {  // no keys: zero rows
-      uint16_t* o = g.out + int64_t(q0s + qt * kBQ + r) * g.o_st + int64_t(h) * g.o_sh;
-      for (int d = 0; d < D; ++d) o[d] = 0;
+    if (qt * kBQ < lq && r < kBQ && qt * kBQ + r < lq) {
+      const int64_t row = q0s + qt * kBQ + r;
+      if (g.splits > 1) {
+        if (row >= g.ws_rows) return;
+        float* rec = g.ws + ((int64_t(split) * g.ws_rows + row) * g.Hq + h) * record_len(D);
+        rec[0] = -INFINITY;
+        for (int d = 1; d < record_len(D); ++d) rec[d] = 0.0f;
+      } else {
+        uint16_t* o = g.out + row * g.o_st + int64_t(h) * g.o_sh;
+        for (int d = 0; d < D; ++d) o[d] = 0;
+      }
     }
     return;
   }
@@ -124,8 +153,6 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
     for (int c = 0; c < DC; ++c) qf[c] = ok ? *reinterpret_cast<const bf16x8_t*>(qp + 16 * c) : bf16x8_t{};
   }
   const int diag = lk - lq;  // query i sees keys <= diag + i
-  const int q_last = min(qt * kBQ + kBQ, lq) - 1;
-  const int k_end = g.causal ? min(lk, diag + q_last + 1) : lk;  // keys this block needs
   const int limit_lane = g.causal ? diag + qi_lane : lk - 1;      // last key of this lane's query
   const int wave_q0 = qt * kBQ + 32 * wave;                        // the wave's first query
 
@@ -307,15 +334,15 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // Two LDS stages: while the waves compute tile i from one, the loads of tile i + 1 (issued a tile earlier) are
   // stored into the other and the loads of tile i + 2 are issued; one barrier per tile. Past the last tile the last
   // one is loaded and stored again, unused (every load is issued unconditionally so the compiler's waits are exact).
-  if (k_end > 0) {
-    const int last = (k_end - 1) / kBK * kBK;
+  {
+    const int last = (k_stop - 1) / kBK * kBK;
     Regs A;
-    gload(A, 0);
+    gload(A, k_beg);
     lstore(A, 0);
     __syncthreads();
-    gload(A, min(kBK, last));
+    gload(A, min(k_beg + kBK, last));
     int stage = 0;
-    for (int kt0 = 0; kt0 < k_end; kt0 += kBK) {
+    for (int kt0 = k_beg; kt0 < k_stop; kt0 += kBK) {
       tile(kt0, stage);
       lstore(A, stage ^ 1);
       gload(A, min(kt0 + 2 * kBK, last));
@@ -328,6 +355,21 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // qi_lane
   l_run = pair32_sum(l_run);
   if (qi_lane >= lq) return;
+  if (g.splits > 1) {  // this split's record of the query: the reference max, the row sum and O, unnormalised
+    if (q0s + qi_lane >= g.ws_rows) return;
+    float* rec = g.ws + ((int64_t(split) * g.ws_rows + q0s + qi_lane) * g.Hq + h) * record_len(D);
+    if (hf == 0) {
+      rec[0] = m_run;
+      rec[1] = l_run;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        *reinterpret_cast<f32x4_t*>(rec + 4 + 32 * t + 8 * rr + 4 * hf) =
+            f32x4_t{o[t][4 * rr], o[t][4 * rr + 1], o[t][4 * rr + 2], o[t][4 * rr + 3]};
+    return;
+  }
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
   uint16_t* op = g.out + int64_t(q0s + qi_lane) * g.o_st + int64_t(h) * g.o_sh + 4 * hf;
 #pragma unroll
@@ -339,20 +381,106 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
                   pack_bf16x2(o[t][4 * rr + 2] * inv, o[t][4 * rr + 3] * inv)};
 }
 
+// Merges the split records of every query of the sequences the prefill kernel took, in split order:
+// O = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s; a query no split saw (M = -inf) is zero.
+// One wave per (query, head), 4 per block (block x: sequence x / per_seq, its (query, head) pairs 4 (x % per_seq)
+// ..): lane s < splits reads split s's max and sum (all at once), the weights are broadcast from those lanes, and
+// each lane sums D / 64 dims over the splits, four splits' loads in flight at a time.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int per_seq) {
+  constexpr int REC = record_len(D), DPL = D / 64;
+  const int b = blockIdx.x / per_seq;
+  const int pr = (blockIdx.x % per_seq) * 4 + int(threadIdx.x) / 64, lane = threadIdx.x % 64;
+  const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
+  if (lq <= g.lq_skip) return;  // the decode kernel wrote these rows (or there are none)
+  const int i = pr / g.Hq, h = pr % g.Hq;
+  if (i >= lq || q0s + i >= g.ws_rows) return;
+  const int64_t step = g.ws_rows * g.Hq * REC;  // one split further
+  const float* rec = g.ws + (int64_t(q0s + i) * g.Hq + h) * REC;
+  const bool mine = lane < g.splits;  // splits <= 64 (host)
+  const float m = mine ? rec[lane * step] : -INFINITY, l = mine ? rec[lane * step + 1] : 0.0f;
+  float M = m;
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) M = fmaxf(M, __shfl_xor(M, off));
+  const float f = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);  // 0 for a split that saw nothing
+  float den = l * f;
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) den += __shfl_xor(den, off);
+  float num[DPL] = {};
+  for (int sp0 = 0; sp0 < g.splits; sp0 += 4) {
+    float v[4][DPL], fs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sp = min(sp0 + u, g.splits - 1);
+      fs[u] = sp0 + u < g.splits ? __shfl(f, sp) : 0.0f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) v[u][e] = rec[sp * step + 4 + lane * DPL + e];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) num[e] = __builtin_fmaf(v[u][e], fs[u], num[e]);
+  }
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  uint16_t* o = g.out + int64_t(q0s + i) * g.o_st + int64_t(h) * g.o_sh + lane * DPL;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) o[e] = f32_to_bf16(num[e] * inv);
+}
+
+// Key splits: only when the blocks of one pass (query tiles x sequences x head groups) leave CUs idle and the
+// sequences bring long key ranges (a chunk of a prompt over its cached prefix, a single long prompt): aiming at
+// ~256 blocks with at least 4 key tiles (256 keys) per split, the longest key range (max_seqlen_k) setting the
+// count.
+void prefill_split_policy(int64_t blocks, int64_t max_seqlen_k, int& splits, int& split_len) {
+  constexpr int64_t kCUs = 256, kMinKeys = 4 * kBK;
+  splits = 1;
+  split_len = int(std::min<int64_t>(std::max<int64_t>(max_seqlen_k, 1), INT32_MAX / 2));
+  if (blocks <= 0 || blocks >= kCUs || max_seqlen_k < 2 * kMinKeys) return;
+  const int64_t want = std::min<int64_t>(std::min<int64_t>((kCUs + blocks - 1) / blocks, max_seqlen_k / kMinKeys), 64);
+  if (want < 2) return;
+  int64_t len = (max_seqlen_k + want - 1) / want;
+  len = (len + kBK - 1) / kBK * kBK;
+  splits = int((max_seqlen_k + len - 1) / len);
+  split_len = int(len);
+}
+
+int prefill_heads_per_block(int64_t Hq, int64_t Hkv) { return (Hq / Hkv) % 2 == 0 ? 2 : 1; }
+
+int64_t prefill_workspace_bytes(int64_t num_seqs, int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t Hq,
+                                int64_t Hkv, int64_t D, int64_t total_q) {
+  const int hb = prefill_heads_per_block(Hq, Hkv);
+  const int64_t qtiles = (max_seqlen_q + block_queries(hb) - 1) / block_queries(hb);
+  int splits, split_len;
+  prefill_split_policy(qtiles * num_seqs * (Hq / hb), max_seqlen_k, splits, split_len);
+  if (splits <= 1) return 0;
+  return int64_t(splits) * total_q * Hq * record_len(int(D)) * int64_t(sizeof(float));
+}
+
 }  // namespace
 }  // namespace nvhip
 
+extern "C" int64_t nvhip_prefill_attention_workspace_size(int64_t num_seqs, int64_t max_seqlen_q,
+                                                          int64_t max_seqlen_k, int64_t Hq, int64_t Hkv, int64_t D,
+                                                          int64_t total_q) {
+  if (num_seqs <= 0 || max_seqlen_q <= 0 || max_seqlen_k <= 0 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 ||
+      (D != 64 && D != 128) || total_q <= 0)
+    return 0;
+  return nvhip::prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
+}
+
 extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void* k, const void* v,
                                             const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                            int64_t num_seqs, int64_t max_seqlen_q, int64_t Hq, int64_t Hkv,
-                                            int64_t D, int64_t q_stride_token, int64_t q_stride_head,
-                                            int64_t k_stride_token, int64_t v_stride_token,
-                                            int64_t out_stride_token, int64_t out_stride_head,
-                                            const int32_t* block_table, int64_t block_size, int64_t num_blocks,
-                                            int64_t max_blocks, float scale, int causal, void* stream) {
+                                            int64_t num_seqs, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                            int64_t total_q, int64_t Hq, int64_t Hkv, int64_t D,
+                                            int64_t q_stride_token, int64_t q_stride_head, int64_t k_stride_token,
+                                            int64_t v_stride_token, int64_t out_stride_token,
+                                            int64_t out_stride_head, const int32_t* block_table, int64_t block_size,
+                                            int64_t num_blocks, int64_t max_blocks, float scale, int causal,
+                                            void* workspace, int64_t workspace_size, void* stream) {
   using namespace nvhip;
   clear_error();
-  if (num_seqs < 0 || max_seqlen_q < 0 || Hq < 1 || Hkv < 1) return invalid("prefill_attention: bad size");
+  if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || total_q < 0 || Hq < 1 || Hkv < 1)
+    return invalid("prefill_attention: bad size");
   if (!(scale > 0.0f) || scale == INFINITY) return invalid("prefill_attention: softmax_scale must be positive");
   if (Hq % Hkv != 0) return invalid("prefill_attention: Hq must be a multiple of Hkv");
   if (D != 64 && D != 128) return invalid("prefill_attention: head_dim must be 64 or 128");
@@ -365,41 +493,53 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
     return invalid("prefill_attention: bad k / v strides");
   if (block_table != nullptr && (block_size < 1 || num_blocks < 1 || max_blocks < 1))
     return invalid("prefill_attention: bad block table shape");
-  if (num_seqs == 0 || max_seqlen_q == 0) return NVHIP_OK;
+  if (num_seqs == 0 || max_seqlen_q == 0 || total_q == 0) return NVHIP_OK;
   if (!out || !q || !k || !v || !cu_seqlens_q || !cu_seqlens_k) return invalid("prefill_attention: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || reinterpret_cast<uintptr_t>(out) % 8)
     return invalid("prefill_attention: q, k, v must be 16-byte and out 8-byte aligned");
-  const int hb = (Hq / Hkv) % 2 == 0 ? 2 : 1;  // q heads per block
+  const int hb = prefill_heads_per_block(Hq, Hkv);  // q heads per block
   const int64_t qtiles = (max_seqlen_q + block_queries(hb) - 1) / block_queries(hb);
   if (qtiles > INT32_MAX || num_seqs > INT32_MAX || num_blocks > INT32_MAX ||
-      max_blocks * block_size > INT32_MAX)
+      max_blocks * block_size > INT32_MAX || max_seqlen_k > INT32_MAX / 2)
     return invalid("prefill_attention: size too large");
-  PrefillArgs g{static_cast<uint16_t*>(out),
-                static_cast<const uint16_t*>(q),
-                static_cast<const uint16_t*>(k),
-                static_cast<const uint16_t*>(v),
-                cu_seqlens_q,
-                cu_seqlens_k,
-                block_table,
-                q_stride_token,
-                q_stride_head,
-                block_table ? Hkv * D : k_stride_token,
-                block_table ? Hkv * D : v_stride_token,
-                out_stride_token,
-                out_stride_head,
-                int(Hkv),
-                int(Hq / Hkv),
-                int(block_size),
-                int(num_blocks),
-                int(max_blocks),
-                scale * 1.4426950408889634f,
-                causal ? 1 : 0,
-                0,
-                0,
-                0};
+  PrefillArgs g{};
+  g.out = static_cast<uint16_t*>(out);
+  g.q = static_cast<const uint16_t*>(q);
+  g.k = static_cast<const uint16_t*>(k);
+  g.v = static_cast<const uint16_t*>(v);
+  g.cu_q = cu_seqlens_q;
+  g.cu_k = cu_seqlens_k;
+  g.bt = block_table;
+  g.q_st = q_stride_token;
+  g.q_sh = q_stride_head;
+  g.k_st = block_table ? Hkv * D : k_stride_token;
+  g.v_st = block_table ? Hkv * D : v_stride_token;
+  g.o_st = out_stride_token;
+  g.o_sh = out_stride_head;
+  g.Hkv = int(Hkv);
+  g.G = int(Hq / Hkv);
+  g.bs = int(block_size);
+  g.num_blocks = int(num_blocks);
+  g.max_blocks = int(max_blocks);
+  g.scale_log2 = scale * 1.4426950408889634f;
+  g.causal = causal ? 1 : 0;
   g.qtiles = int(qtiles);
   g.nhg = int(Hq / hb);
-  const int64_t blocks = qtiles * num_seqs * (Hq / hb);
+  g.lq_skip = 0;
+  g.Hq = int(Hq);
+  g.ws_rows = total_q;
+  const int64_t base_blocks = qtiles * num_seqs * (Hq / hb);
+  // split the keys over several blocks when the caller gave a large enough workspace
+  g.splits = 1;
+  g.split_len = int(std::max<int64_t>(max_seqlen_k, 1));
+  const int64_t need = prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
+  if (need > 0 && workspace && workspace_size >= need) {
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+      return invalid("prefill_attention: workspace must be 16-byte aligned");
+    prefill_split_policy(base_blocks, max_seqlen_k, g.splits, g.split_len);
+    g.ws = static_cast<float*>(workspace);
+  }
+  const int64_t blocks = base_blocks * g.splits;
   if (blocks > INT32_MAX) return invalid("prefill_attention: size too large");
   const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kThreads));
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -428,5 +568,12 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   else if (paged) NVHIP_PREFILL_LAUNCH(128, true, 1);
   else NVHIP_PREFILL_LAUNCH(128, false, 1);
 #undef NVHIP_PREFILL_LAUNCH
-  return check_launch("prefill_attention");
+  if (int rc = check_launch("prefill_attention")) return rc;
+  if (g.splits == 1) return NVHIP_OK;
+  const int64_t per_seq = (max_seqlen_q * Hq + 3) / 4;  // blocks of 4 (query, head) waves per sequence
+  if (num_seqs * per_seq > INT32_MAX) return invalid("prefill_attention: size too large");
+  const dim3 cgrid(static_cast<unsigned>(num_seqs * per_seq));
+  if (D == 64) hipLaunchKernelGGL((prefill_combine<64>), cgrid, dim3(256), 0, s, g, int(per_seq));
+  else hipLaunchKernelGGL((prefill_combine<128>), cgrid, dim3(256), 0, s, g, int(per_seq));
+  return check_launch("prefill_attention (combine)");
 }

@@ -71,4 +71,4 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
         q = q.contiguous()
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     return torch.ops.nvhip.prefill_attention(q, k, v, cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous(),
-                                             int(max_seqlen_q), scale, causal, block_table)
+                                             int(max_seqlen_q), int(max_seqlen_k), scale, causal, block_table)

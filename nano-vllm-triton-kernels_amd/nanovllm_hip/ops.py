@@ -26,7 +26,7 @@ _DEF.define("matmul_silu_mul(Tensor a, Tensor w) -> Tensor")
 _DEF.define("rms_norm_matmul(Tensor x, Tensor? residual, Tensor norm_w, float eps, Tensor w, bool silu) "
             "-> (Tensor, Tensor)")
 _DEF.define("prefill_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
-            "int max_seqlen_q, float scale, bool causal, Tensor? block_table) -> Tensor")
+            "int max_seqlen_q, int max_seqlen_k, float scale, bool causal, Tensor? block_table) -> Tensor")
 _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
             "Tensor slot_mapping) -> ()")
 _DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
@@ -261,7 +261,8 @@ def _rms_norm_matmul_fake(x, residual, norm_w, eps, w, silu):
 
 # ------------------------------------------------------------------ prefill (varlen) attention
 
-def _prefill_attention_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, scale, causal, block_table):
+def _prefill_attention_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal,
+                            block_table):
     Tq, Hq, D = q.shape
     out = torch.empty((Tq, Hq, D), dtype=q.dtype, device=q.device)
     if block_table is None:
@@ -270,10 +271,15 @@ def _prefill_attention_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, s
     else:
         Hkv, bt, bs, nb, mb = k.shape[2], block_table.data_ptr(), k.shape[1], k.shape[0], block_table.shape[1]
         k_st = v_st = Hkv * D
-    status = _lib.lib().nvhip_prefill_attention_bf16(
+    num_seqs = cu_seqlens_q.shape[0] - 1
+    lib = _lib.lib()
+    ws_bytes = lib.nvhip_prefill_attention_workspace_size(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, Tq)
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    status = lib.nvhip_prefill_attention_bf16(
         out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
-        cu_seqlens_q.shape[0] - 1, max_seqlen_q, Hq, Hkv, D, q.stride(0), q.stride(1), k_st, v_st, out.stride(0),
-        out.stride(1), bt, bs, nb, mb, scale, int(causal), _lib.stream_of(q))
+        num_seqs, max_seqlen_q, max_seqlen_k, Tq, Hq, Hkv, D, q.stride(0), q.stride(1), k_st, v_st, out.stride(0),
+        out.stride(1), bt, bs, nb, mb, scale, int(causal), ws.data_ptr() if ws is not None else None,
+        ws_bytes if ws is not None else 0, _lib.stream_of(q))
     _lib.check(status, "prefill_attention")
     return out
 
@@ -282,5 +288,6 @@ _DEF.impl("prefill_attention", _prefill_attention_impl, "CUDA")
 
 
 @torch.library.register_fake("nvhip::prefill_attention")
-def _prefill_attention_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, scale, causal, block_table):
+def _prefill_attention_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal,
+                            block_table):
     return torch.empty(q.shape, dtype=q.dtype, device=q.device)

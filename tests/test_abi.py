@@ -112,9 +112,10 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
 
     pre = lib.nvhip_prefill_attention_bf16
 
-    def prefill(num_seqs=2, maxq=64, Hq=16, Hkv=8, D=128, kst=4160, bt=None, bs=0, nb=0, mb=0, scale=0.1):
-        return pre(P, P, P, P, P, P, num_seqs, maxq, Hq, Hkv, D, 4160, 128, kst, kst, 2048, 128, bt, bs, nb, mb,
-                   scale, 1, P)
+    def prefill(num_seqs=2, maxq=64, Hq=16, Hkv=8, D=128, kst=4160, bt=None, bs=0, nb=0, mb=0, scale=0.1,
+                ws=None, ws_size=0):
+        return pre(P, P, P, P, P, P, num_seqs, maxq, 300, 128, Hq, Hkv, D, 4160, 128, kst, kst, 2048, 128, bt, bs,
+                   nb, mb, scale, 1, ws, ws_size, P)
 
     assert prefill(D=256) == _lib.NVHIP_EINVAL and "head_dim" in _err()
     assert prefill(kst=1000) == _lib.NVHIP_EINVAL and "k / v strides" in _err()
@@ -123,6 +124,15 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
     assert prefill(scale=0.0) == _lib.NVHIP_EINVAL and "softmax_scale" in _err()
     assert prefill(scale=-0.1) == _lib.NVHIP_EINVAL and "softmax_scale" in _err()
     assert prefill() == _lib.NVHIP_EINVAL and "null" in _err()
+
+    # key splits of the prefill attention: only when few blocks meet long key ranges
+    pws = lib.nvhip_prefill_attention_workspace_size
+    rec = (128 + 4) * 4                                       # bytes of one (split, query, head) record
+    assert pws(4, 2048, 2048, 16, 8, 128, 8192) == 0          # 4 x 16 query tiles x 8 head pairs: CUs full
+    assert pws(1, 256, 300, 16, 8, 128, 256) == 0             # keys too few to split
+    assert pws(1, 256, 4096, 16, 8, 128, 256) == 16 * 256 * 16 * rec    # chunk over a prefix: 16 splits of 256
+    assert pws(1, 2048, 2048, 16, 8, 128, 2048) == 2 * 2048 * 16 * rec  # one long prompt: 2 splits of 1024
+    assert pws(1, 256, 4096, 16, 8, 256, 256) == 0            # head_dim 256 is not supported
 
     st = lib.nvhip_store_kvcache
     assert st(P, P, P, P, 1024, 1024, P, 64, 4, 1024, 3, P) == _lib.NVHIP_EINVAL and "element size" in _err()

@@ -6,7 +6,8 @@ atol 1e-2. Cases: a Qwen3-0.6B prefill batch (16 q / 8 kv heads, head_dim 128, k
 projection output), the prefix cache (keys through a block table of 256- and 16-slot blocks, NaN in unused slots),
 head_dim 64, GQA ratios 1 / 4 / 8, non-causal, more queries than keys (rows that see nothing are zero), an empty
 sequence, graph capture and replay; mixed steps over the cache, whose sequences with <= 16 / G queries run in the
-paged decode kernel (bitwise the decode attention's rows for one-query sequences).
+paged decode kernel (bitwise the decode attention's rows for one-query sequences); chunks over long prefixes and
+long prompts whose keys are split over blocks and merged (with and without the cache, causal and not, in graphs).
 """
 import numpy as np
 import pytest
@@ -139,6 +140,57 @@ def test_decode_only_varlen_equals_decode_attention():
                                   torch.tensor(lk, dtype=torch.int32, device=DEV), bt.to(DEV), 128 ** -0.5,
                                   causal=True)
     assert torch.equal(out, dec.view(-1, 16, 128).cpu())
+
+
+def test_chunk_over_a_long_prefix_splits_the_keys():
+    """A 256-token chunk over 3840 cached keys: 16 blocks would stream 4096 keys each, so the call splits the keys
+    into 16 ranges (256 blocks) and merges them (workspace query pinned on the CPU)."""
+    from nanovllm_hip import _lib
+    assert _lib.lib().nvhip_prefill_attention_workspace_size(1, 256, 4096, 16, 8, 128, 256) > 0
+    q, kc, vc, bt = paged_case([256], [4096], 256, seed=21)
+    check(q, kc, vc, cu([256]), cu([4096]), True, bt)
+
+
+def test_split_keys_with_decode_rows_and_causal_limits():
+    """Key splits together with the short-sequence path in one call over the cache: one-query sequences, a chunk
+    over a long prefix and a sequence whose later splits see no key for its first queries."""
+    lq = [1, 1, 300, 1, 40]
+    lk = [900, 50, 3000, 2000, 1200]
+    q, kc, vc, bt = paged_case(lq, lk, 16, seed=22)
+    check(q, kc, vc, cu(lq), cu(lk), True, bt)
+
+
+def test_split_keys_without_cache_non_causal_and_head_dim_64():
+    # one fresh 1100-token prompt (9 query tiles x 8 head pairs: 4 key splits), causal
+    _, q, k, v = contiguous_case([1100], seed=23)
+    check(q.contiguous(), k.contiguous(), v.contiguous(), cu([1100]), cu([1100]))
+    # non-causal, head_dim 64, 4 q heads per kv head: 100 queries over 1500 keys
+    g = torch.Generator("cpu").manual_seed(24)
+    q = torch.randn(100, 16, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(1500, 4, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(1500, 4, 64, generator=g).to(torch.bfloat16)
+    check(q, k, v, cu([100]), cu([1500]), causal=False)
+
+
+def test_split_graph_replay_matches_eager():
+    q, kc, vc, bt = paged_case([256], [4096], 256, seed=25)
+    q, kc, vc, bt = q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV)
+    cq, ck = cu([256]).to(DEV), cu([4096]).to(DEV)
+    eager = flash_attn_varlen_func(q, kc, vc, 256, cq, 4096, ck, 0.1, True, bt)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        flash_attn_varlen_func(q, kc, vc, 256, cq, 4096, ck, 0.1, True, bt)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = flash_attn_varlen_func(q, kc, vc, 256, cq, 4096, ck, 0.1, True, bt)
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
 
 
 def test_head_dim_64_and_gqa():
