@@ -16,7 +16,8 @@ T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNo
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
 the paged decode attention of one layer for 32 sequences with contexts of 512..2048 tokens, in GB/s; the causal
-prefill attention of one layer over 4 sequences of 2048 tokens, in TFLOP/s; the end-to-end decode step of a
+prefill attention of one layer over 4 sequences of 2048 tokens and of a 256-token chunk over 3840 cached keys, in
+TFLOP/s; the end-to-end decode step of a
 random-init Qwen3-0.6B-shaped model (batch 32, HIP graph: us per step, tokens/s, kernel nodes); a 256-token mixed
 step of the same model (16 decode requests + a 240-token prefill chunk), eager and from piecewise graphs.
 The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
@@ -227,6 +228,7 @@ def extras(torch, oracle, kernels, dev, steps):
         del a, w0, ws
     out["paged_decode_attention_B32"] = decode_attention(torch, dev, steps, g)
     out["prefill_attention_4x2048"] = prefill_attention(torch, dev, steps, g)
+    out["prefill_chunk256_over_3840"] = prefill_chunk_over_prefix(torch, dev, steps, g)
     n = 4096
     a = torch.randn(n, n, generator=g).to(dev)
     b = torch.randn(n, n, generator=g).to(dev)
@@ -289,6 +291,26 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048, profile=False):
     ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True), 4,
                        max(20, steps // 4), 4, WARM_S)
     flops = 4 * D * HQ * nseq * L * (L + 1) // 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+def prefill_chunk_over_prefix(torch, dev, steps, g, chunk=256, prefix=3840):
+    """Causal attention of one Qwen3-0.6B layer for a `chunk`-token piece of a prompt over its `prefix` cached keys
+    (chunked prefill / prefix cache: the keys come through a block table of the paged 256-slot cache). flops = 4 *
+    D * Hq * sum over the chunk's queries of the keys each sees."""
+    from nanovllm_hip.kernels.attention import flash_attn_varlen_func
+    lk = prefix + chunk
+    nb = (lk + BLOCK - 1) // BLOCK
+    kc = torch.randn(nb, BLOCK, HKV, D, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(nb, BLOCK, HKV, D, generator=g).to(torch.bfloat16).to(dev)
+    bt = torch.randperm(nb, generator=g).to(torch.int32).view(1, nb).to(dev)
+    q = torch.randn(chunk, HQ, D, generator=g).to(torch.bfloat16).to(dev)
+    cq = torch.tensor([0, chunk], dtype=torch.int32, device=dev)
+    ck = torch.tensor([0, lk], dtype=torch.int32, device=dev)
+    ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, kc, vc, chunk, cq, lk, ck, D ** -0.5, True, bt), 4,
+                       max(20, steps // 4), 4, WARM_S)
+    flops = 4 * D * HQ * sum(prefix + i + 1 for i in range(chunk))
     tf = flops / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
