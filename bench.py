@@ -24,7 +24,8 @@ The CPU baseline is the oracle (the reference's torch code restated, fp32 math, 
 sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 8192] [--no-cpu] [--no-extra] [--no-e2e]
-       (profiling modes: --profile, --profile-gemm, --profile-e2e, --profile-prefill, --profile-mixed)
+       (profiling modes: --profile, --profile-gemm, --profile-e2e, --profile-prefill, --profile-chunk,
+       --profile-mixed)
 """
 import argparse
 import json
@@ -295,7 +296,7 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048, profile=False):
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
-def prefill_chunk_over_prefix(torch, dev, steps, g, chunk=256, prefix=3840):
+def prefill_chunk_over_prefix(torch, dev, steps, g, chunk=256, prefix=3840, profile=False):
     """Causal attention of one Qwen3-0.6B layer for a `chunk`-token piece of a prompt over its `prefix` cached keys
     (chunked prefill / prefix cache: the keys come through a block table of the paged 256-slot cache). flops = 4 *
     D * Hq * sum over the chunk's queries of the keys each sees."""
@@ -308,6 +309,12 @@ def prefill_chunk_over_prefix(torch, dev, steps, g, chunk=256, prefix=3840):
     q = torch.randn(chunk, HQ, D, generator=g).to(torch.bfloat16).to(dev)
     cq = torch.tensor([0, chunk], dtype=torch.int32, device=dev)
     ck = torch.tensor([0, lk], dtype=torch.int32, device=dev)
+    if profile:  # for a rocprofv3 kernel trace: `steps` eager calls, nothing else launched
+        for _ in range(steps):
+            flash_attn_varlen_func(q, kc, vc, chunk, cq, lk, ck, D ** -0.5, True, bt)
+        torch.cuda.synchronize()
+        print(f"profile: {steps} prefill attention calls ({chunk}-token chunk over {prefix} cached keys)", flush=True)
+        return None
     ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, kc, vc, chunk, cq, lk, ck, D ** -0.5, True, bt), 4,
                        max(20, steps // 4), 4, WARM_S)
     flops = 4 * D * HQ * sum(prefix + i + 1 for i in range(chunk))
@@ -451,6 +458,9 @@ def main():
     p.add_argument("--profile-prefill", action="store_true",
                    help="for rocprofv3 kernel traces: --steps eager launches of the prefill attention (4 x 2048 "
                         "tokens, one Qwen3-0.6B layer)")
+    p.add_argument("--profile-chunk", action="store_true",
+                   help="for rocprofv3 kernel traces: --steps eager calls of the prefill attention for a 256-token "
+                        "chunk over 3840 cached keys (one Qwen3-0.6B layer)")
     p.add_argument("--profile-mixed", action="store_true",
                    help="for rocprofv3 kernel traces: build the model, prefill 16 requests, then time the 256-token "
                         "mixed step (16 decodes + a 240-token chunk) --steps times eagerly and --steps times from "
@@ -477,6 +487,9 @@ def main():
         return
     if args.profile_prefill:
         prefill_attention(torch, dev, args.steps, torch.Generator().manual_seed(0), profile=True)
+        return
+    if args.profile_chunk:
+        prefill_chunk_over_prefix(torch, dev, args.steps, torch.Generator().manual_seed(0), profile=True)
         return
     if args.profile_mixed:
         print(json.dumps(e2e_mixed_step(torch, dev, reps=args.steps)), flush=True)

@@ -548,7 +548,8 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   // requests of a mixed step -- run in the paged decode kernel, one block per (sequence, kv head) streaming its
   // keys; the prefill kernel's blocks for them return at once.
   const int64_t G = Hq / Hkv;
-  if (paged && G <= 16) {
+  // (one sequence with more queries than that: nothing for the decode kernel, no launch)
+  if (paged && G <= 16 && !(num_seqs == 1 && total_q > 16 / G)) {
     g.lq_skip = int(std::min<int64_t>(16 / G, max_seqlen_q));
     if (int rc = paged_decode_varlen(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(q),
                                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), block_table,
