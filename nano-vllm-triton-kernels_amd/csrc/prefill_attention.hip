@@ -453,6 +453,8 @@ int64_t prefill_workspace_bytes(int64_t num_seqs, int64_t max_seqlen_q, int64_t 
   int splits, split_len;
   prefill_split_policy(qtiles * num_seqs * (Hq / hb), max_seqlen_k, splits, split_len);
   if (splits <= 1) return 0;
+  const double bytes = double(splits) * double(total_q) * double(Hq) * record_len(int(D)) * sizeof(float);
+  if (bytes > double(int64_t(1) << 40)) return 0;  // no split rather than a workspace past 1 TiB
   return int64_t(splits) * total_q * Hq * record_len(int(D)) * int64_t(sizeof(float));
 }
 
