@@ -7,7 +7,8 @@ projection output), the prefix cache (keys through a block table of 256- and 16-
 head_dim 64, GQA ratios 1 / 4 / 8, non-causal, more queries than keys (rows that see nothing are zero), an empty
 sequence, graph capture and replay; mixed steps over the cache, whose sequences with <= 16 / G queries run in the
 paged decode kernel (bitwise the decode attention's rows for one-query sequences); chunks over long prefixes and
-long prompts whose keys are split over blocks and merged (with and without the cache, causal and not, in graphs).
+long prompts whose keys are split over blocks and merged (with and without the cache, causal and not, in graphs);
+seeded random batches over the cache.
 """
 import numpy as np
 import pytest
@@ -191,6 +192,27 @@ def test_split_graph_replay_matches_eager():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_varlen_batches(seed):
+    """Seeded random batches over the cache: 1-6 sequences mixing empty, one-query, short (<= 16 / G queries, the
+    decode kernel's) and long query runs over prefixes of 0-1200 cached keys; block sizes 16 / 64 / 256; GQA ratios
+    1 / 2 / 4; head_dim 64 / 128; causal or not. Some batches split their keys over blocks."""
+    rng = np.random.default_rng(1000 + seed)
+    Hq, Hkv = [(16, 8), (8, 8), (16, 4)][seed % 3]
+    D = 128 if seed % 2 == 0 else 64
+    bs = [16, 64, 256][seed % 3]
+    n = int(rng.integers(1, 7))
+    lq, lk = [], []
+    for _ in range(n):
+        kind = rng.integers(0, 4)
+        q = [0, 1, int(rng.integers(2, 9)), int(rng.integers(9, 200))][kind]
+        lq.append(q)
+        lk.append(q + int(rng.integers(0, 1201)))
+    causal = bool(seed % 4 != 3)
+    q, kc, vc, bt = paged_case(lq, lk, bs, Hq=Hq, Hkv=Hkv, D=D, seed=2000 + seed)
+    check(q, kc, vc, cu(lq), cu(lk), causal, bt)
 
 
 def test_head_dim_64_and_gqa():
