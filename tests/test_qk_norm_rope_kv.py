@@ -209,6 +209,20 @@ def test_head_layouts(hq, hkv, d):
     check_case(Case(37, seed=hq * 7 + hkv + d, hq=hq, hkv=hkv, d=d))
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_layouts(seed):
+    """Seeded random cases: token counts 1-700, head layouts including very wide ones (more than 1024 / (D / 16)
+    rows per token: the flattened (token, row) kernel), row padding, 2-byte-offset views and random slots / -1
+    padding."""
+    rng = np.random.default_rng(500 + seed)
+    layouts = [(16, 8, 128), (128, 8, 128), (64, 8, 256), (6, 2, 64), (32, 4, 128), (8, 8, 256), (96, 16, 128),
+               (2, 2, 64)]
+    hq, hkv, d = layouts[seed]
+    tokens = int(rng.integers(1, 701))
+    check_case(Case(tokens, seed=3000 + seed, hq=hq, hkv=hkv, d=d, pad=int(rng.integers(0, 3)) * 8,
+                    offset=int(seed % 4 == 1)))
+
+
 def test_unaligned_views():
     # q/k/v start 2 bytes into the buffer: the kernel takes its unaligned (2-byte access) path
     check_case(Case(45, seed=5, offset=1, pad=3))
