@@ -143,6 +143,8 @@ class Piecewise:
         Padded rows (token 0 at position 0) never reach the attention: it gets the first n rows, writes no KV for
         the rest, and their attention output is zero."""
         n = input_ids.shape[0]
+        if n > self.buckets[-1]:  # the reference runs such a step eagerly, unpadded (model_runner.py:516-519)
+            raise ValueError(f"{n} tokens exceed the largest bucket ({self.buckets[-1]}): run model.forward")
         bucket = next(b for b in self.buckets if b >= n)
         self.input_ids[:n] = input_ids
         self.input_ids[n:bucket] = 0
