@@ -90,8 +90,8 @@ def mixed_buckets(max_num_batched_tokens=512):
 class Piecewise:
     """Runs mixed steps of `model` segment by segment (model_runner.py:543-591): segment 0 = embedding + layer 0 up
     to its attention, segment i = the rest of layer i - 1 + layer i up to its attention, segment L = the rest of
-    the last layer + the final norm. With use_graphs the segments of each bucket are recorded once (record()) and
-    replayed; without, the same code runs eagerly on the same padded shapes (the reference's enforce_eager)."""
+    the last layer + the final norm. After record() the segments of each bucket are replayed from their graphs;
+    before, the same code runs eagerly on the same padded shapes (the reference's enforce_eager)."""
 
     def __init__(self, model: Qwen3, buckets, backend="hip", linear="hip", attention="hip"):
         c = model.cfg
