@@ -7,7 +7,8 @@
 //
 // Fast path (n a multiple of 8, 16-byte aligned rows): the [rows, n/8] space of 8-element vectors is flattened;
 // a 256-thread block takes VPT runs of 256 consecutive vectors, each thread one vector per run (gate and up are
-// two 16-byte loads, the output one 16-byte store). The row of a vector comes from a multiply-shift division.
+// two 16-byte loads, the output one 16-byte nontemporal store). The row of a vector comes from a multiply-shift
+// division.
 #include "common.h"
 
 namespace nvhip {
@@ -60,7 +61,8 @@ __global__ __launch_bounds__(kBlock) void silu_mul_kernel(const SiluArgs a) {
     unpack8(up[k], u);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = silu_bf16(g[i]) * u[i];
-    store8<true>(a.out + int64_t(row[k]) * a.n + col[k], pack8(o));
+    // the output is not read again by this kernel: streamed with the nontemporal hint (~4 % faster at 151 MB)
+    __builtin_nontemporal_store(pack8(o), reinterpret_cast<u32x4*>(a.out + int64_t(row[k]) * a.n + col[k]));
   }
 }
 
