@@ -70,6 +70,18 @@ __device__ __forceinline__ float pair32_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// gfx950 transpose read ds_read_b64_tr_b16 from a row-major bf16 tile in LDS: within each 16-lane group, lane i
+// receives element i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3, its 4 bf16 in that order;
+// measured with an in-bounds one-wave probe). Lanes 4j .. 4j+3 addressing row j and 16 consecutive columns hand
+// lane i column i of the 4 rows: the layout of an MFMA A/B operand read from a key-major tile.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // 8 bf16 (16 bytes) <-> 8 fp32.
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 #pragma unroll

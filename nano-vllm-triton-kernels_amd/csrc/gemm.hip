@@ -129,7 +129,6 @@ __global__ __launch_bounds__(kBlock) void gemm_generic(const GemmArgs g) {
 // load as zero (K a multiple of 8); otherwise K is a multiple of 64 * RS.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGroupM = 8;

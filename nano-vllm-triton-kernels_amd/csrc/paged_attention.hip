@@ -90,15 +90,6 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
   return ((int64_t(blk) * g.bs + t % g.bs) * g.Hkv + kvh) * D;
 }
 
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// 4 bf16 of the A operand from a row-major tile in LDS (see step 4): the 8-byte chunk this lane addresses is
-// transposed with those of the other lanes of its 16-lane group.
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
-  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p));
-  return __builtin_bit_cast(u32x2, v);
-}
 
 template <int D, int RP, bool ALIGNED>
 __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const DecodeArgs g) {

@@ -11,8 +11,7 @@
 // One block (8 waves) per (query tile, sequence, pair of q heads of one kv head): 4 waves and 128 queries per head;
 // when Hq / Hkv is odd, one head per block with 8 waves and 256 queries. Wave w of a head owns queries 32w .. 32w+31
 // of the tile. The two heads share the K/V tiles (half the K/V traffic of a block per head). Per 64-key tile:
-//   1. the K tile goes to LDS key-major ([64][D], 16-byte chunks, rows padded), the V tile dim-major ([D][64],
-//      transposed on the way in, so that a lane's keys of one dim are contiguous);
+//   1. the K and V tiles go to LDS key-major ([64][D], 16-byte chunks, rows padded);
 //   2. S^T [32 keys x 32 queries] = K Q^T per 32-key half with v_mfma_f32_32x32x16_bf16 (K rows from LDS as the A
 //      operand, the wave's Q rows from registers as the B operand): lane l holds keys 8 (r / 4) + 4 (l / 32) + r % 4
 //      (register r) of query l % 32, so one query's 64 scores sit in lanes l and l ^ 32;
@@ -20,8 +19,9 @@
 //      one FMA and the hardware exp;
 //   4. O^T [32 dims x 32 queries] += V^T P^T per 32-dim tile and 16-key step: P (bf16) stays in the registers it was
 //      computed in as the B operand, whose 8 k slots of lane l are the keys 4 (l / 32) .. +3 and 8 + 4 (l / 32) ..
-//      +3 of the step; the A operand reads the same keys of dim l % 32 from the transposed V tile (two 8-byte LDS
-//      reads). Each lane keeps one query's O, so the rescale by 2^(m_old - m_new) is lane-local.
+//      +3 of the step; the A operand gets the same keys of dim l % 32 from the key-major V tile with two gfx950
+//      transpose reads (ds_read_b64_tr_b16, 4 keys each). Each lane keeps one query's O, so the rescale by
+//      2^(m_old - m_new) is lane-local.
 // A wave's 32 queries use each K and V fragment it reads from LDS twice as often as 16 would, which halves the LDS
 // reads per flop; the per-tile work that does not scale with the queries (loads, LDS stores, barriers) is shared by
 // twice the flops.
@@ -40,7 +40,6 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kWavesBlock = 8;  // waves per block: 4 per head with two heads, 8 with one
@@ -90,8 +89,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   constexpr int DT = D / 32;   // 32-dim output tiles
   constexpr int CPR = D / 8;   // 16-byte chunks per K/V row
   constexpr int KP = D + 8;    // K row pitch (elements)
-  constexpr int VP = kBK + 4;  // V^T row pitch: the 32 rows of a fragment read start 34 banks apart (no conflict)
-  constexpr int STAGE = kBK * KP + D * VP;  // elements of one LDS stage (K tile, then V^T tile)
+  // V row pitch: D + 32 elements puts the 4 rows of a transpose read 16 (or 48) banks apart, so the 32 lanes of a
+  // half-wave (4 keys x 32 dims) hit 64 distinct banks
+  constexpr int VP = D + 32;
+  constexpr int STAGE = kBK * (KP + VP);  // elements of one LDS stage (K tile, then V tile)
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
   // Block order. The ids are dealt round-robin over the 8 XCDs (block b runs on XCD b % 8) and each XCD starts its
@@ -162,78 +163,71 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   float m_run = -INFINITY, l_run = 0.0f;
 
   // 1. a tile's K and V chunks go global -> registers (all loads of a tile issued together; the next tile's loads
-  // are issued before this tile's MFMAs) -> LDS. K chunk c: key c / CPR, dims (c % CPR) * 8, stored key-major; V
-  // chunk c: key c % 64, dims (c / 64) * 8, stored transposed (a wave's lanes take consecutive keys of one dim
-  // chunk, so the 2-byte LDS writes of a lane group are contiguous). Invalid keys read the first 16 bytes of q and
-  // store zeros.
+  // are issued before this tile's MFMAs) -> LDS. K and V chunk c: key c / CPR, dims (c % CPR) * 8, stored
+  // key-major with one 16-byte write. Invalid keys read the first 16 bytes of q and store zeros.
   constexpr int NT = kThreads;              // threads loading the tiles
   constexpr int NL = kBK * CPR / NT;        // chunks per thread per operand
   static_assert(NL >= 1 && NL * NT == kBK * CPR, "tile chunks per thread");
   struct Regs {
     u32x4 k[NL], v[NL];
-    uint32_t kok, vok;
+    uint32_t kok;  // bit i: the key of chunk i is valid (its K and V rows were read)
     bool all;  // every key of the tile is valid (wave-uniform): no zeroing at the LDS store
   };
   const int32_t* bt_row = PAGED ? g.bt + int64_t(b) * g.max_blocks : nullptr;
   // Contiguous keys: this thread's K / V row addresses at key tile 0; tile kt0 adds kt0 rows (a scalar offset).
   const uint16_t* kbase[NL];
-  const uint16_t* vbase = nullptr;
+  const uint16_t* vbase[NL];
   if constexpr (!PAGED) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * NT;
       kbase[i] = g.k + int64_t(k0s + c / CPR) * g.k_st + int64_t(kvh) * D + (c % CPR) * 8;
+      vbase[i] = g.v + int64_t(k0s + c / CPR) * g.v_st + int64_t(kvh) * D + (c % CPR) * 8;
     }
-    vbase = g.v + int64_t(k0s + tid % kBK) * g.v_st + int64_t(kvh) * D;
   }
   auto gload = [&](Regs& R, int kt0) {
-    const int vj = kt0 + tid % kBK;  // V chunks of a thread share one key (NT is a multiple of kBK)
     R.all = kt0 + kBK <= lk;
-    R.kok = R.vok = 0;
+    R.kok = 0;
     if constexpr (!PAGED) {
       if (R.all) {  // every row valid: the addresses are the bases plus a per-tile offset
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
           R.k[i] = *reinterpret_cast<const u32x4*>(kbase[i] + int64_t(kt0) * g.k_st);
-          R.v[i] = *reinterpret_cast<const u32x4*>(vbase + int64_t(kt0) * g.v_st + ((tid + i * NT) / kBK) * 8);
+          R.v[i] = *reinterpret_cast<const u32x4*>(vbase[i] + int64_t(kt0) * g.v_st);
         }
         return;
       }
     }
     // block-table entries of this thread's keys first (PAGED), then every data load back to back
-    int kblk[NL], vblk = 0;
+    int kblk[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int kj = kt0 + (tid + i * NT) / CPR;
       kblk[i] = PAGED && kj < lk ? bt_row[kj / g.bs] : 0;
     }
-    if constexpr (PAGED) vblk = vj < lk ? bt_row[vj / g.bs] : 0;
-    const int64_t vrow = vj < lk ? key_row<D, PAGED>(g, k0s, vj, vblk, kvh, g.v_st) : -1;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * NT;
       const int kj = kt0 + c / CPR;
       const int64_t krow = kj < lk ? key_row<D, PAGED>(g, k0s, kj, kblk[i], kvh, g.k_st) : -1;
-      R.kok |= uint32_t(krow >= 0) << i;
-      R.vok |= uint32_t(vrow >= 0) << i;
+      const int64_t vrow = kj < lk ? key_row<D, PAGED>(g, k0s, kj, kblk[i], kvh, g.v_st) : -1;
+      R.kok |= uint32_t(krow >= 0) << i;  // krow and vrow are valid together
       R.k[i] = *reinterpret_cast<const u32x4*>(krow >= 0 ? g.k + krow + (c % CPR) * 8 : g.q);
-      R.v[i] = *reinterpret_cast<const u32x4*>(vrow >= 0 ? g.v + vrow + (c / kBK) * 8 : g.q);
+      R.v[i] = *reinterpret_cast<const u32x4*>(vrow >= 0 ? g.v + vrow + (c % CPR) * 8 : g.q);
     }
     if constexpr (PAGED) R.all = false;  // a block-table entry may be invalid
   };
   auto lstore = [&](const Regs& R, int stage) {
     uint16_t* Ks = lds + stage * STAGE;
-    uint16_t* Vt = Ks + kBK * KP;
+    uint16_t* Vs = Ks + kBK * KP;
     const bool all = R.all;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * NT;
       const u32x4 zero = u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&Ks[(c / CPR) * KP + (c % CPR) * 8]) = (all || ((R.kok >> i) & 1)) ? R.k[i] : zero;
-      const u32x4 x = (all || ((R.vok >> i) & 1)) ? R.v[i] : zero;
-      const int key = c % kBK, dc = (c / kBK) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(dc + e) * VP + key] = uint16_t(x[e / 2] >> (16 * (e & 1)));
+      const bool ok = all || ((R.kok >> i) & 1);
+      *reinterpret_cast<u32x4*>(&Ks[(c / CPR) * KP + (c % CPR) * 8]) = ok ? R.k[i] : zero;
+      *reinterpret_cast<u32x4*>(&Vs[(c / CPR) * VP + (c % CPR) * 8]) = ok ? R.v[i] : zero;
     }
   };
 
@@ -244,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   constexpr float kLazy = 8.0f;
   auto tile = [&](int kt0, int stage) {
     const uint16_t* Ks = lds + stage * STAGE;
-    const uint16_t* Vt = Ks + kBK * KP;
+    const uint16_t* Vs = Ks + kBK * KP;
     // S^T per 32-key half: lane holds keys kt0 + 32 u + 8 (r / 4) + 4 hf + r % 4 of query qi_lane. All K fragments
     // of the tile are read before the first MFMA, so the MFMAs wait for LDS latency once, not once each.
     bf16x8_t kf[2][DC];
@@ -261,7 +255,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
       for (int c = 0; c < DC; ++c) s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[u][c], qf[c], s[u], 0, 0, 0);
     }
     // V^T fragments of both halves (A operands of O^T += V^T P^T): dim 32 t + l % 32, keys 32 u + 16 j + 4 hf .. +3
-    // and 32 u + 16 j + 8 + 4 hf .. +3; read here so that they are in flight during the softmax
+    // and 32 u + 16 j + 8 + 4 hf .. +3, by transpose reads (lane i of a 16-lane group addresses key i / 4 of the 4,
+    // dims 4 (i % 4) .. +3 of the group's 16, and receives dim i of the 4 keys); read here so that they are in flight
+    // during the softmax
+    const uint16_t* vt0 = Vs + (4 * hf + (lane % 16) / 4) * VP + 16 * (ql / 16) + 4 * (lane % 4);
     u32x4 vf[2][DT][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -269,9 +266,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
       for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const uint16_t* vr = &Vt[(32 * t + ql) * VP + 32 * u + 16 * j + 4 * hf];
-          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
-          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 8);
+          const uint16_t* vr = vt0 + (32 * u + 16 * j) * VP + 32 * t;
+          const u32x2 lo = lds_read_tr16(vr), hi = lds_read_tr16(vr + 8 * VP);
           vf[u][t][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
     // issue order: the 8 K reads of half 0, then its MFMAs each followed by a K read of half 1, the MFMAs of half 1,
@@ -376,8 +372,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr)
-      *reinterpret_cast<u32x2_t*>(op + 32 * t + 8 * rr) =
-          u32x2_t{pack_bf16x2(o[t][4 * rr] * inv, o[t][4 * rr + 1] * inv),
+      *reinterpret_cast<u32x2*>(op + 32 * t + 8 * rr) =
+          u32x2{pack_bf16x2(o[t][4 * rr] * inv, o[t][4 * rr + 1] * inv),
                   pack_bf16x2(o[t][4 * rr + 2] * inv, o[t][4 * rr + 3] * inv)};
 }
 
