@@ -231,10 +231,11 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
     }
   };
 
-  // 2.-4. per 32-key half u of a tile: S^T, online softmax, O^T += V^T P^T. The two halves are separate softmax
-  // steps so that the VALU work of one overlaps the MFMAs of the other. Rescaling is lazy: a query's reference max
-  // m_run only moves when a score exceeds it by more than kLazy (base 2), so p <= 2^kLazy; O and the row sum carry
-  // the same factor, which cancels in O / sum, and almost every tile after the first skips the O rescale.
+  // 2.-4. per tile: S^T of both 32-key halves, one online-softmax step over the tile's 64 keys, O^T += V^T P^T
+  // (the p of the second half are computed under the P.V MFMAs of the first). Rescaling is lazy: a query's
+  // reference max m_run only moves when a score exceeds it by more than kLazy (base 2), so p <= 2^kLazy; O and the
+  // row sum carry the same factor, which cancels in O / sum, and almost every tile after the first skips the O
+  // rescale (one wave-uniform branch per tile).
   constexpr float kLazy = 8.0f;
   auto tile = [&](int kt0, int stage) {
     const uint16_t* Ks = lds + stage * STAGE;
@@ -270,20 +271,26 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
           const u32x2 lo = lds_read_tr16(vr), hi = lds_read_tr16(vr + 8 * VP);
           vf[u][t][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
-    // issue order: the 8 K reads of half 0, then its MFMAs each followed by a K read of half 1, the MFMAs of half 1,
-    // then the V reads
+    // issue order: the 8 K reads of half 0, then its MFMAs each followed by a K read of half 1, then the MFMAs of
+    // half 1 interleaved with the max of half 0 (VALU work under the matrix cores), then the V reads
     __builtin_amdgcn_sched_group_barrier(0x100, DC, 0);
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, DC, 0);
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
     __builtin_amdgcn_sched_group_barrier(0x100, 4 * DT, 0);
     // Only a tile that reaches past the key count or past the causal limit of the wave's first query needs the
     // mask (wave-uniform test); key offsets within the tile are compile-time constants per register.
     const bool full = kt0 + kBK <= lk && (!g.causal || kt0 + kBK - 1 <= diag + wave_q0);
     const int lim = min(lk - 1, limit_lane) - kt0 - 4 * hf;  // largest visible offset 32 u + 8 (r / 4) + r % 4
+    // max of the tile's raw scores (the scale is positive)
+    float tmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       if (!full) {
@@ -291,23 +298,24 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
         for (int r = 0; r < 16; ++r)
           if (32 * u + 8 * (r / 4) + r % 4 > lim) s[u][r] = -INFINITY;
       }
-      // max of the raw scores (the scale is positive), then p = 2^(s * scale_log2 - m) in one FMA and v_exp_f32
-      // (arguments <= kLazy; only results below the fp32 normal range, which flush to 0, differ from exp2f)
-      float tmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
-      tmax = pair32_max(tmax) * g.scale_log2;
-      const bool move = tmax > m_run + kLazy;  // also true for the first finite max (m_run = -inf)
-      if (__ballot(move) != 0) {
-        const float alpha = move ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.0f;  // 0 from m_run = -inf
-        if (move) m_run = tmax;
-        l_run *= alpha;
+    }
+    tmax = pair32_max(tmax) * g.scale_log2;
+    const bool move = tmax > m_run + kLazy;  // also true for the first finite max (m_run = -inf)
+    if (__ballot(move) != 0) {
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.0f;  // 0 from m_run = -inf
+      if (move) m_run = tmax;
+      l_run *= alpha;
 #pragma unroll
-        for (int t = 0; t < DT; ++t) o[t] *= alpha;
-      }
-      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-      // p as bf16, packed per 16-key step (registers 8 j .. 8 j + 7) in the k-slot order of P.V
-      bf16x8_t pf[2];
+      for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // p = 2^(s * scale_log2 - m) in one FMA and v_exp_f32 (arguments <= kLazy; only results below the fp32 normal
+    // range, which flush to 0, differ from exp2f), as bf16 packed per 16-key step in the k-slot order of P.V
+    bf16x8_t pf[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         float p[8];
@@ -316,15 +324,22 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
           p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][8 * j + e], g.scale_log2, -m_use));
           l_run += p[e];
         }
-        pf[j] = __builtin_bit_cast(bf16x8_t, pack8(p));
+        pf[u][j] = __builtin_bit_cast(bf16x8_t, pack8(p));
       }
-      // O^T += V^T P^T
+    // O^T += V^T P^T; the p of half 1 are computed under the MFMAs of half 0
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[u][t][j]), pf[j], o[t], 0, 0,
-                                                         0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[u][t][j]), pf[u][j], o[t], 0,
+                                                         0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 28, 1);
+#pragma unroll
+    for (int i = 0; i < 2 * DT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
     }
   };
   // Two LDS stages: while the waves compute tile i from one, the loads of tile i + 1 (issued a tile earlier) are
