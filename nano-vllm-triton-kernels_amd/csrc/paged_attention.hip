@@ -314,24 +314,55 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
 template <int D, int RP>
 __global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) {
   const int pair = blockIdx.x, b = pair / g.Hkv, kvh = pair % g.Hkv;
-  const int rows = g.G * g.q_len;
+  int q0 = b * g.q_len, lq = g.q_len;  // as in paged_decode_kernel
+  if (g.cu_q != nullptr) {
+    q0 = g.cu_q[b];
+    lq = g.cu_q[b + 1] - q0;
+    if (lq < 1 || lq > g.q_len) return;  // no records: the kernel's blocks left this sequence alone
+  }
+  const int rows = g.G * lq;
   for (int idx = threadIdx.x; idx < rows * D; idx += 256) {
     const int r = idx / D, d = idx % D;
     const float* rec = g.ws + (int64_t(pair) * g.splits * RP + r) * (2 + D);
     const int64_t step = int64_t(RP) * (2 + D);
-    float M = -INFINITY;
-    for (int sp = 0; sp < g.splits; ++sp) M = fmaxf(M, rec[sp * step]);
     float num = 0.0f, den = 0.0f;
-    if (M != -INFINITY) {
-      for (int sp = 0; sp < g.splits; ++sp) {
-        const float f = exp2f(rec[sp * step] - M);
-        num = __builtin_fmaf(rec[sp * step + 2 + d], f, num);
-        den = __builtin_fmaf(rec[sp * step + 1], f, den);
+    if (g.splits <= 4) {  // every load of the (max, sum, O) records issued at once
+      float m[4], l[4], o[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        m[u] = -INFINITY, l[u] = o[u] = 0.0f;
+        if (u < g.splits) {
+          m[u] = rec[u * step];
+          l[u] = rec[u * step + 1];
+          o[u] = rec[u * step + 2 + d];
+        }
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) M = fmaxf(M, m[u]);
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (u >= g.splits) break;
+          const float f = exp2f(m[u] - M);
+          num = __builtin_fmaf(o[u], f, num);
+          den = __builtin_fmaf(l[u], f, den);
+        }
+      }
+    } else {
+      float M = -INFINITY;
+      for (int sp = 0; sp < g.splits; ++sp) M = fmaxf(M, rec[sp * step]);
+      if (M != -INFINITY) {
+        for (int sp = 0; sp < g.splits; ++sp) {
+          const float f = exp2f(rec[sp * step] - M);
+          num = __builtin_fmaf(rec[sp * step + 2 + d], f, num);
+          den = __builtin_fmaf(rec[sp * step + 1], f, den);
+        }
       }
     }
     const float o = den > 0.0f ? num / den : 0.0f;
     const int i = r / g.G, hh = r % g.G;
-    g.out[int64_t(b * g.q_len + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
+    g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
   }
 }
 
@@ -381,10 +412,18 @@ int64_t workspace_bytes(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv
 
 }  // namespace
 
+int64_t paged_decode_varlen_workspace(int64_t num_seqs, int64_t qmax, int64_t Hq, int64_t Hkv, int64_t D) {
+  // split_policy makes at most ceil(256 / pairs) splits, whatever the context length
+  const int64_t pairs = std::max<int64_t>(1, num_seqs * Hkv), most = (256 + pairs - 1) / pairs;
+  if (most <= 1 || qmax < 1 || Hkv < 1) return 0;
+  return num_seqs * Hkv * most * rows_padded((Hq / Hkv) * qmax) * (2 + D) * int64_t(sizeof(float));
+}
+
 int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                         const int32_t* block_table, const int32_t* cu_q, const int32_t* cu_k, int num_seqs, int qmax,
                         int Hq, int Hkv, int D, int block_size, int num_blocks, int max_blocks, int64_t q_st,
-                        int64_t q_sh, int64_t o_st, int64_t o_sh, float scale, int causal, hipStream_t s) {
+                        int64_t q_sh, int64_t o_st, int64_t o_sh, float scale, int causal, float* ws, int64_t ws_bytes,
+                        hipStream_t s) {
   const int G = Hq / Hkv, rows = G * qmax;
   if (qmax < 1 || rows > 16 || (D != 64 && D != 128 && D != 256) ||
       int64_t(num_seqs) * Hkv > INT32_MAX || int64_t(max_blocks) * block_size > INT32_MAX)
@@ -392,6 +431,17 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
   DecodeArgs g{out, q, k_cache, v_cache, block_table, nullptr, qmax, Hkv, G, block_size, num_blocks, max_blocks,
                q_st, q_sh, o_st, o_sh, scale * 1.4426950408889634f, causal ? 1 : 0, 1,
                max_blocks * block_size, nullptr, cu_q, cu_k};
+  // the decode entry point's key splits (same policy, so its one-query rows stay bitwise those of a decode call)
+  if (ws != nullptr && ws_bytes > 0) {
+    int splits, split_len;
+    split_policy(num_seqs, Hkv, int64_t(max_blocks) * block_size, splits, split_len);
+    const int64_t need = int64_t(num_seqs) * Hkv * splits * rows_padded(rows) * (2 + D) * int64_t(sizeof(float));
+    if (splits > 1 && ws_bytes >= need && int64_t(num_seqs) * Hkv * splits <= INT32_MAX) {
+      g.splits = splits;
+      g.split_len = split_len;
+      g.ws = ws;
+    }
+  }
   switch (D) {
     case 64: return launch_decode_rows<64>(g, num_seqs, rows, s);
     case 128: return launch_decode_rows<128>(g, num_seqs, rows, s);

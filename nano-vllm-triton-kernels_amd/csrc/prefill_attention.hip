@@ -469,6 +469,25 @@ int64_t prefill_workspace_bytes(int64_t num_seqs, int64_t max_seqlen_q, int64_t 
   return int64_t(splits) * total_q * Hq * record_len(int(D)) * int64_t(sizeof(float));
 }
 
+// Queries per sequence the paged decode kernel takes in a call with a block table (0: none): sequences with at
+// most 16 / G queries, unless the call has one sequence with more (nothing for that kernel then).
+int64_t short_queries(int64_t num_seqs, int64_t total_q, int64_t Hq, int64_t Hkv, int64_t max_seqlen_q) {
+  const int64_t G = Hq / Hkv;
+  if (G > 16 || (num_seqs == 1 && total_q > 16 / G)) return 0;
+  return std::min<int64_t>(16 / G, max_seqlen_q);
+}
+
+// Workspace: the prefill kernel's split records, then (16-byte aligned) those of the paged decode kernel's splits.
+int64_t decode_workspace_offset(int64_t prefill_bytes) { return (prefill_bytes + 15) / 16 * 16; }
+
+int64_t total_workspace_bytes(int64_t num_seqs, int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t Hq, int64_t Hkv,
+                              int64_t D, int64_t total_q) {
+  const int64_t pre = prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
+  const int64_t qs = short_queries(num_seqs, total_q, Hq, Hkv, max_seqlen_q);
+  const int64_t dec = qs > 0 ? paged_decode_varlen_workspace(num_seqs, qs, Hq, Hkv, D) : 0;
+  return dec > 0 ? decode_workspace_offset(pre) + dec : pre;
+}
+
 }  // namespace
 }  // namespace nvhip
 
@@ -478,7 +497,7 @@ extern "C" int64_t nvhip_prefill_attention_workspace_size(int64_t num_seqs, int6
   if (num_seqs <= 0 || max_seqlen_q <= 0 || max_seqlen_k <= 0 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 ||
       (D != 64 && D != 128) || total_q <= 0)
     return 0;
-  return nvhip::prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
+  return nvhip::total_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
 }
 
 extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void* k, const void* v,
@@ -546,9 +565,9 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   g.splits = 1;
   g.split_len = int(std::max<int64_t>(max_seqlen_k, 1));
   const int64_t need = prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
+  if (workspace && reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return invalid("prefill_attention: workspace must be 16-byte aligned");
   if (need > 0 && workspace && workspace_size >= need) {
-    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
-      return invalid("prefill_attention: workspace must be 16-byte aligned");
     prefill_split_policy(base_blocks, max_seqlen_k, g.splits, g.split_len);
     g.ws = static_cast<float*>(workspace);
   }
@@ -560,15 +579,19 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   // With the cache (a mixed step, a prefix-cache chunk), sequences with at most 16 / G queries -- the decode
   // requests of a mixed step -- run in the paged decode kernel, one block per (sequence, kv head) streaming its
   // keys; the prefill kernel's blocks for them return at once.
-  const int64_t G = Hq / Hkv;
-  // (one sequence with more queries than that: nothing for the decode kernel, no launch)
-  if (paged && G <= 16 && !(num_seqs == 1 && total_q > 16 / G)) {
-    g.lq_skip = int(std::min<int64_t>(16 / G, max_seqlen_q));
+  const int64_t qs = paged ? short_queries(num_seqs, total_q, Hq, Hkv, max_seqlen_q) : 0;
+  if (qs > 0) {
+    g.lq_skip = int(qs);
+    // its key splits use the part of the workspace after the prefill kernel's records
+    const int64_t off = decode_workspace_offset(need);
+    float* dws = workspace && workspace_size > off ? reinterpret_cast<float*>(static_cast<char*>(workspace) + off)
+                                                   : nullptr;
     if (int rc = paged_decode_varlen(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(q),
                                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), block_table,
                                      cu_seqlens_q, cu_seqlens_k, int(num_seqs), g.lq_skip, int(Hq), int(Hkv), int(D),
                                      int(block_size), int(num_blocks), int(max_blocks), q_stride_token,
-                                     q_stride_head, out_stride_token, out_stride_head, scale, causal, s))
+                                     q_stride_head, out_stride_token, out_stride_head, scale, causal, dws,
+                                     dws ? workspace_size - off : 0, s))
       return rc;
     if (max_seqlen_q <= g.lq_skip) return NVHIP_OK;
   }

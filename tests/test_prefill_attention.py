@@ -143,6 +143,21 @@ def test_decode_only_varlen_equals_decode_attention():
     assert torch.equal(out, dec.view(-1, 16, 128).cpu())
 
 
+def test_few_decode_sequences_split_like_the_decode_call():
+    """5 one-query sequences (40 (sequence, kv head) pairs, fewer than the CUs): the varlen call's short-sequence
+    path splits the contexts over blocks with the decode call's policy and workspace layout, so its rows stay
+    bitwise those of flash_attn_with_kvcache, which splits them too."""
+    from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
+    lk = [2000, 37, 1025, 512, 1800]
+    lq = [1] * len(lk)
+    q, kc, vc, bt = paged_case(lq, lk, 256, seed=13)
+    out, _ = check(q, kc, vc, cu(lq), cu(lk), True, bt)
+    dec = flash_attn_with_kvcache(q.to(DEV).view(len(lk), 1, 16, 128), kc.to(DEV), vc.to(DEV),
+                                  torch.tensor(lk, dtype=torch.int32, device=DEV), bt.to(DEV), 128 ** -0.5,
+                                  causal=True)
+    assert torch.equal(out, dec.view(-1, 16, 128).cpu())
+
+
 def test_chunk_over_a_long_prefix_splits_the_keys():
     """A 256-token chunk over 3840 cached keys: 16 blocks would stream 4096 keys each, so the call splits the keys
     into 16 ranges (256 blocks) and merges them (workspace query pinned on the CPU)."""
