@@ -197,6 +197,28 @@ int64_t nvhip_prefill_attention_workspace_size(int64_t num_seqs, int64_t max_seq
 int64_t nvhip_paged_decode_attention_workspace_size(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv,
                                                     int64_t D, int64_t block_size, int64_t max_blocks);
 
+/*
+ * A projection followed by the Add+RMSNorm that consumes it (o_proj -> post_attention_layernorm, down_proj -> the
+ * next layer's input_layernorm in models/qwen3.py:176-209): h = bf16(x W^T), s = fp32(h) + fp32(residual),
+ * residual_out = bf16(s), y = bf16(bf16(s * rstd) * norm_w) -- nvhip_matmul then nvhip_add_rms_norm_bf16.
+ * Not in the reference's kernels: the epilogue side of the GEMM fusions of matmul.py:3-4, for the longer inputs of
+ * mixed steps and prompt chunks (M > 32). When the product's 64x64 tiles leave CUs idle (N = 1024 / 2048 / 4096,
+ * M up to a few hundred) its K is split over up to 4 block ranges whose fp32 partial products the norm kernel sums
+ * in split order before rounding h to bf16: no extra launch, and h then differs from nvhip_matmul's only by that
+ * summation order (within fp32 rounding; deterministic). Otherwise the two launches, bitwise.
+ *   x [M, K] row stride x_stride, W [N, K] row stride w_stride (K-contiguous, 16-byte aligned rows, K % 8 == 0);
+ *   residual, residual_out and y [M, N] contiguous, 16-byte aligned (residual_out may be residual); norm_w [N].
+ *   workspace: at least nvhip_matmul_add_rms_norm_workspace_size(M, N, K) bytes, 16-byte aligned (required;
+ *   contents need no initialisation). Calls that share a workspace must be ordered on one stream.
+ */
+int nvhip_matmul_add_rms_norm_bf16(void* y, void* residual_out, const void* x, const void* weight,
+                                   const void* residual, const void* norm_w, float eps, int64_t M, int64_t N,
+                                   int64_t K, int64_t x_stride, int64_t w_stride, void* workspace,
+                                   int64_t workspace_size, void* stream);
+
+/* Bytes of workspace nvhip_matmul_add_rms_norm_bf16 needs for these sizes. Host-only, no GPU work. */
+int64_t nvhip_matmul_add_rms_norm_workspace_size(int64_t M, int64_t N, int64_t K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,13 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
 // independent of the context lengths.
 int64_t paged_decode_varlen_workspace(int64_t num_seqs, int64_t qmax, int64_t Hq, int64_t Hkv, int64_t D);
 
+// Add+RMSNorm (rms_norm.hip) of rows whose x is the sum of `splits` (1..4) fp32 partial products [splits, rows, n]
+// (a split-K GEMM's): x = bf16(partials summed in split order), then exactly nvhip_add_rms_norm_bf16 with a
+// contiguous residual (res_out may alias r). Only for the n add_rms_norm_partials_supported accepts.
+bool add_rms_norm_partials_supported(int64_t n);
+int add_rms_norm_partials(uint16_t* y, uint16_t* res_out, const float* xp, int splits, const uint16_t* r,
+                          const uint16_t* w, int64_t rows, int64_t n, float eps, hipStream_t s);
+
 // ---------------------------------------------------------------- device: bf16 <-> fp32
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));

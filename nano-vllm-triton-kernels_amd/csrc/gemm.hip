@@ -140,6 +140,8 @@ struct MfmaArgs {
   const uint16_t* w;  // B^T: element (n, k) at w + n*swn + k
   int M, N, K;
   int64_t sam, swn, scm;
+  int splits = 1;      // PARTIAL kernels: K ranges; block b computes range b % splits of tile b / splits
+  float* ws = nullptr; // PARTIAL kernels: fp32 partial products [splits, M, N]
 };
 
 __device__ __forceinline__ void tile_coords(int pid, int M, int N, int BM, int BN, int& pid_m, int& pid_n) {
@@ -168,7 +170,10 @@ __device__ __forceinline__ void unroll_steps(F& step, int kt) {
 // SILU: W is [2 * N2, K] = [gate; up] (N = 2 * N2) and C is [M, N2] = bf16(silu(A Wg^T)) * bf16(A Wu^T) rounded
 // to bf16: a tile's first BN / 2 B rows are gate rows n0 / 2 .., the last BN / 2 the matching up rows N2 + n0 / 2 ..
 // (so the per-column k order is that of the plain product, and the result is bitwise the unfused one).
-template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU = false>
+// PARTIAL (split-K, for launches with few tiles): the block's K range is z * K / splits .. (z + 1) * K / splits and
+// its fp32 tile goes unrounded to ws[z] (N a multiple of BN, K / splits a multiple of 64 * RS); the consumer sums
+// the splits in order.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU = false, bool PARTIAL = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const MfmaArgs g) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
@@ -184,8 +189,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   constexpr int LPK = (CH + 3) / 4;       // chunks refilled from global memory per k step (k steps 0..3)
   __shared__ __attribute__((aligned(16))) uint16_t smem[LDS_ELEMS];
 
+  int pid = blockIdx.x, z = 0;
+  if constexpr (PARTIAL) {
+    z = pid % g.splits;
+    pid /= g.splits;
+  }
+  const int kspan = PARTIAL ? g.K / g.splits : g.K, kbeg = z * kspan;
   int pid_m, pid_n;
-  tile_coords(blockIdx.x, g.M, g.N, BM, BN, pid_m, pid_n);
+  tile_coords(pid, g.M, g.N, BM, BN, pid_m, pid_n);
   const int m0 = pid_m * BM, n0 = pid_n * BN;
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -203,7 +214,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
       const int n2 = g.N / 2, half = BN / 2;
       wrow = row < half ? min(n0 / 2 + row, n2 - 1) : n2 + min(n0 / 2 + row - half, n2 - 1);
     }
-    src[i] = isA ? g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + kc * 8 : g.w + int64_t(wrow) * g.swn + kc * 8;
+    src[i] = (isA ? g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam : g.w + int64_t(wrow) * g.swn) + kbeg + kc * 8;
     dst[i] = (isA ? 0 : BM * kBK) + row * kBK + ((kc ^ ((row >> 1) & 7)) * 8);
     kofs[i] = kc * 8;
   }
@@ -219,7 +230,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x16_t{};
 
   const int frag_row = lane % 32, frag_half = lane / 32, swz = (frag_row >> 1) & 7;
-  const int nk = (g.K + kBK - 1) / kBK;
+  const int nk = (kspan + kBK - 1) / kBK;
   // prologue: k-tile 0 -> LDS stage 0; k-tiles 1..RS in flight in the register slots
 #pragma unroll
   for (int i = 0; i < CH; ++i) r[0][i] = gload1(i, 0);
@@ -286,6 +297,30 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   for (int kt = 0; kt < nk; kt += RS) unroll_steps<0, RS>(step, kt);  // nk % RS == 0 (checked on the host)
   __syncthreads();
 
+  if constexpr (PARTIAL) {  // fp32 tile -> LDS -> coalesced 16-byte row stores into ws[z]
+    constexpr int FP = BN + 4;
+    static_assert(BM * FP * 4 <= LDS_ELEMS * 2, "fp32 tile fits the LDS");
+    float* ft = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int run = 0; run < 4; ++run) {
+          const int rr = wm * WM + i * 32 + frag_row, col = wn * WN + j * 32 + 8 * run + 4 * frag_half;
+          *reinterpret_cast<f32x4_t*>(&ft[rr * FP + col]) =
+              f32x4_t{acc[i][j][4 * run], acc[i][j][4 * run + 1], acc[i][j][4 * run + 2], acc[i][j][4 * run + 3]};
+        }
+    __syncthreads();
+    float* wz = g.ws + int64_t(z) * g.M * g.N;
+    for (int c = tid; c < BM * (BN / 4); c += NT) {
+      const int rr = c / (BN / 4), cc = (c % (BN / 4)) * 4;
+      if (m0 + rr >= g.M) continue;
+      *reinterpret_cast<f32x4_t*>(wz + int64_t(m0 + rr) * g.N + n0 + cc) =
+          *reinterpret_cast<const f32x4_t*>(&ft[rr * FP + cc]);
+    }
+    return;
+  }
   // epilogue: accumulators -> bf16 tile in LDS -> coalesced 16-byte row stores
   uint16_t* ot = smem;
 #pragma unroll
@@ -962,4 +997,76 @@ extern "C" int nvhip_rms_norm_matmul_bf16(void* out, void* residual_out, const v
   if (add) NVHIP_NORM_MM(false, 4, true);
   NVHIP_NORM_MM(false, 4, false);
 #undef NVHIP_NORM_MM
+}
+
+namespace nvhip {
+namespace {
+
+// K ranges of the product in nvhip_matmul_add_rms_norm_bf16: when its 64x64 tiles leave CUs idle (M of a mixed step
+// or a prompt chunk, N = hidden), each tile's K is split in up to 4 ranges so that every CU streams a part -- the
+// blocks of a few-tile launch each wait on their chain of K / 64 k-tiles -- and the Add+RMSNorm that consumes the
+// product sums the fp32 partials (no extra launch). Each range is a whole number of 4-k-tile rounds (RS = 4).
+int norm_splits(int64_t M, int64_t N, int64_t K) {
+  if (M <= 32 || M >= (int64_t(1) << 31) || N % 64 != 0 || K % kBK != 0 || K >= (int64_t(1) << 31) ||
+      !add_rms_norm_partials_supported(N))
+    return 1;
+  const int64_t tiles = (M + 63) / 64 * (N / 64);
+  if (tiles >= 256) return 1;
+  for (int s = int(std::min<int64_t>(4, 256 / tiles)); s > 1; --s)
+    if (K % (int64_t(kBK) * 4 * s) == 0) return s;
+  return 1;
+}
+
+int64_t matmul_norm_workspace(int64_t M, int64_t N, int64_t K) {
+  const int s = norm_splits(M, N, K);
+  const int64_t bytes = s > 1 ? int64_t(s) * M * N * 4 : M * N * 2;
+  return (bytes + 15) / 16 * 16;
+}
+
+}  // namespace
+}  // namespace nvhip
+
+extern "C" int64_t nvhip_matmul_add_rms_norm_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return nvhip::matmul_norm_workspace(M, N, K);
+}
+
+extern "C" int nvhip_matmul_add_rms_norm_bf16(void* y, void* residual_out, const void* x, const void* weight,
+                                              const void* residual, const void* norm_w, float eps, int64_t M,
+                                              int64_t N, int64_t K, int64_t x_stride, int64_t w_stride,
+                                              void* workspace, int64_t workspace_size, void* stream) {
+  using namespace nvhip;
+  clear_error();
+  if (M < 0 || N <= 0 || K <= 0) return invalid("matmul_add_rms_norm: bad shape");
+  if (x_stride < K || w_stride < K || x_stride % 8 != 0 || w_stride % 8 != 0 || K % 8 != 0)
+    return invalid("matmul_add_rms_norm: x / weight rows must be K-contiguous, 16-byte aligned, K % 8 == 0");
+  if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31) || K >= (int64_t(1) << 31))
+    return invalid("matmul_add_rms_norm: size too large");
+  if (M == 0) return NVHIP_OK;
+  if (!y || !residual_out || !x || !weight || !residual || !norm_w || !workspace)
+    return invalid("matmul_add_rms_norm: null pointer");
+  if (!aligned16(y) || !aligned16(residual_out) || !aligned16(x) || !aligned16(weight) || !aligned16(residual) ||
+      !aligned16(norm_w) || !aligned16(workspace))
+    return invalid("matmul_add_rms_norm: pointers must be 16-byte aligned");
+  if (workspace_size < matmul_norm_workspace(M, N, K))
+    return invalid("matmul_add_rms_norm: workspace smaller than nvhip_matmul_add_rms_norm_workspace_size");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MfmaArgs m{nullptr, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), int(M), int(N), int(K),
+             x_stride, w_stride, N};
+  const int splits = norm_splits(M, N, K);
+  if (splits > 1) {  // split-K partials, summed by the norm
+    m.splits = splits;
+    m.ws = static_cast<float*>(workspace);
+    const int64_t blocks = (M + 63) / 64 * (N / 64) * splits;
+    hipLaunchKernelGGL((gemm_mfma_nt<64, 64, 2, 2, 4, false, false, true>), dim3(unsigned(blocks)), dim3(256), 0, s,
+                       m);
+    if (int rc = check_launch("matmul_add_rms_norm")) return rc;
+    return add_rms_norm_partials(static_cast<uint16_t*>(y), static_cast<uint16_t*>(residual_out), m.ws, splits,
+                                 static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(norm_w), M, N,
+                                 eps, s);
+  }
+  // the bf16 product in the workspace, then the Add+RMSNorm: bitwise matmul followed by add_rms_norm
+  m.c = static_cast<uint16_t*>(workspace);
+  if (int rc = launch_mfma_auto<false>(m, s)) return rc;
+  return nvhip_add_rms_norm_bf16(y, residual_out, workspace, residual, norm_w, M, N, N, N, eps, stream);
 }

@@ -27,9 +27,14 @@ struct NormArgs {
   int64_t x_stride, r_stride;                              // row strides (add_rms_norm)
   int64_t n;
   float inv_n, eps;
+  // add_rms_norm with x given as splits (1..4) fp32 partial products [splits, rows, n] (split s at xp + s * xp_split):
+  // x = bf16(sum of the partials in split order), the rounding of the GEMM output they add up to
+  const float* xp;
+  int splits;
+  int64_t xp_split;
 };
 
-template <int LANES, int VPL, bool ADD>
+template <int LANES, int VPL, bool ADD, bool PART = false>
 __global__ __launch_bounds__(kBlock) void norm_kernel(const NormArgs a) {
   constexpr int N = LANES * VPL * 8;
   const int sub = threadIdx.x % LANES;
@@ -48,8 +53,34 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const NormArgs a) {
 
   float v[VPL][8];
   u32x4 raw[VPL], wraw[VPL];
+  if constexpr (PART) {  // every split's vectors loaded at once, then summed in split order and rounded to bf16
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const float* xp = a.xp + row * a.n;
+    f32x4 p[4][VPL][2];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) raw[j] = load8<true>(xr + (j * LANES + sub) * 8);
+    for (int s = 0; s < 4; ++s)
+      if (s < a.splits)
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            p[s][j][h] = *reinterpret_cast<const f32x4*>(xp + s * a.xp_split + (j * LANES + sub) * 8 + 4 * h);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = p[0][j][i / 4][i % 4];
+#pragma unroll
+      for (int s = 1; s < 4; ++s)
+        if (s < a.splits)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] += p[s][j][i / 4][i % 4];
+      raw[j] = pack8(x);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) raw[j] = load8<true>(xr + (j * LANES + sub) * 8);
+  }
   // the weight is loaded up front: after the residual store the compiler could not move it past a possible alias
 #pragma unroll
   for (int j = 0; j < VPL; ++j) wraw[j] = load8<true>(a.w + (j * LANES + sub) * 8);
@@ -130,11 +161,11 @@ __global__ __launch_bounds__(kBlock) void norm_kernel_generic(const NormArgs a) 
   }
 }
 
-template <bool ADD, int LANES, int VPL>
+template <bool ADD, int LANES, int VPL, bool PART = false>
 int launch_fast(const NormArgs& a, hipStream_t s) {
   const int64_t rows_per_block = kBlock / LANES;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((norm_kernel<LANES, VPL, ADD>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL((norm_kernel<LANES, VPL, ADD, PART>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
   return check_launch(ADD ? "add_rms_norm" : "rms_norm");
 }
 
@@ -165,6 +196,24 @@ int launch_norm(const NormArgs& a, bool aligned, hipStream_t s) {
 }
 
 }  // namespace
+
+bool add_rms_norm_partials_supported(int64_t n) { return n == 1024 || n == 2048 || n == 4096; }
+
+int add_rms_norm_partials(uint16_t* y, uint16_t* res_out, const float* xp, int splits, const uint16_t* r,
+                          const uint16_t* w, int64_t rows, int64_t n, float eps, hipStream_t s) {
+  if (!add_rms_norm_partials_supported(n) || splits < 1 || splits > 4)
+    return invalid("add_rms_norm (partials): unsupported size");
+  NormArgs a{};
+  a.y = y, a.res_out = res_out, a.r = r, a.w = w;
+  a.rows = rows, a.r_stride = n, a.n = n, a.inv_n = 1.0f / float(n), a.eps = eps;
+  a.xp = xp, a.splits = splits, a.xp_split = rows * n;
+  switch (n) {
+    case 1024: return launch_fast<true, 64, 2, true>(a, s);
+    case 2048: return launch_fast<true, 64, 4, true>(a, s);
+    default: return launch_fast<true, 64, 8, true>(a, s);
+  }
+}
+
 }  // namespace nvhip
 
 extern "C" int nvhip_rms_norm_bf16(void* y, const void* x, const void* w, int64_t groups, int64_t rows_per_group,

@@ -172,6 +172,15 @@ def hip_linear(x, w):
     return hip.matmul(x, w.t())
 
 
+@dataclass
+class Deferred:
+    """The projection x @ weight^T, not computed yet: post_attn hands its down projection to the Add+RMSNorm that
+    consumes it (the next layer's input norm or the final norm), which runs both in one call
+    (hip.matmul_add_rms_norm)."""
+    x: torch.Tensor
+    weight: torch.Tensor
+
+
 # ------------------------------------------------------------------ the model
 
 class Qwen3:
@@ -223,6 +232,9 @@ class Qwen3:
             if residual is None:
                 residual = h
                 qkv = hip.rms_norm_matmul(h, L["input_norm"], eps, L["qkv"])
+            elif isinstance(h, Deferred):  # the previous layer's down projection, then this norm, then qkv
+                h, residual = hip.matmul_add_rms_norm(h.x, h.weight, residual, L["input_norm"], eps)
+                qkv = hip_linear(h, L["qkv"])
             else:
                 qkv, residual = hip.add_rms_norm_matmul(h, residual, L["input_norm"], eps, L["qkv"])
         else:
@@ -279,11 +291,17 @@ class Qwen3:
 
     def post_attn(self, li, o, residual, backend, linear="hip"):
         """Layer li after its attention (models/qwen3.py:199-209): o_proj, the post-attention norm and the MLP.
-        Returns (h, residual); like pre_attn it reads nothing of the batch layout."""
+        Returns (h, residual); like pre_attn it reads nothing of the batch layout. With the hip backend and GEMM
+        and more than 32 tokens, o_proj runs with the norm that consumes it and h is the down projection Deferred
+        to the next norm (pre_attn / final_norm), which runs with it."""
         c, L = self.cfg, self.layers[li]
         eps, hq, D = c.rms_norm_eps, c.num_attention_heads, c.head_dim
         lin = hip_linear if backend == "hip" and linear == "hip" else F.linear
-        h = lin(o.reshape(o.shape[0], hq * D), L["o"])
+        o2 = o.reshape(o.shape[0], hq * D)
+        if backend == "hip" and linear == "hip" and o2.shape[0] > 32:
+            h, residual = hip.matmul_add_rms_norm(o2, L["o"], residual, L["post_norm"], eps)
+            return Deferred(hip.matmul_silu_and_mul(h, L["gate_up"]), L["down"]), residual
+        h = lin(o2, L["o"])
         if backend == "hip" and linear == "hip":   # norm, gate_up and SiLU x Mul in one launch for decode batches
             h, residual = hip.add_rms_norm_matmul(h, residual, L["post_norm"], eps, L["gate_up"], silu=True)
         elif backend == "hip":
@@ -297,6 +315,8 @@ class Qwen3:
 
     def final_norm(self, h, residual, backend):
         """The model's last Add+RMSNorm (models/qwen3.py:232) -> hidden states [T, hidden]."""
+        if isinstance(h, Deferred):
+            return hip.matmul_add_rms_norm(h.x, h.weight, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]
         if backend == "hip":
             return hip.fused_add_rms_norm_(h, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]
         return add_rms_forward(h, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]

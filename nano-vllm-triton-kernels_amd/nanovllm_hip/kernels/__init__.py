@@ -3,8 +3,8 @@
 `backend` plays the role of nanovllm/kernels/__init__.py:5: the layers read it once when they are built and
 dispatch on it ("hip" selects these kernels; "compile" keeps the layers' own torch code).
 """
-from nanovllm_hip.kernels.matmul import (add_rms_norm_matmul, matmul, matmul_silu_and_mul,  # noqa: F401
-                                          rms_norm_matmul)
+from nanovllm_hip.kernels.matmul import (add_rms_norm_matmul, matmul, matmul_add_rms_norm,  # noqa: F401
+                                          matmul_silu_and_mul, rms_norm_matmul)
 from nanovllm_hip.kernels.qk_norm_rope_kv import qk_norm_rope_kv  # noqa: F401
 from nanovllm_hip.kernels.rms_norm import fused_add_rms_norm, fused_add_rms_norm_, rms_norm  # noqa: F401
 from nanovllm_hip.kernels.store_kvcache import store_kvcache  # noqa: F401

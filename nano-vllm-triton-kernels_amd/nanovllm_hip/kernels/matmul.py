@@ -55,6 +55,27 @@ def rms_norm_matmul(x: torch.Tensor, norm_w: torch.Tensor, eps: float, weight: t
     return out
 
 
+def matmul_add_rms_norm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor,
+                        eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """fused_add_rms_norm(matmul(x, weight.t()), residual, norm_w, eps) -> (normed, new residual): a projection
+    and the Add+RMSNorm that consumes it (o_proj -> post_attention_layernorm, down_proj -> the next
+    input_layernorm, models/qwen3.py:176-209). For inputs whose 64x64 tiles leave CUs idle (M of a mixed step or
+    a prompt chunk, hidden 1024 / 2048 / 4096) the projection's K is split over blocks and the norm kernel sums the
+    fp32 partial products before rounding them to bf16 (deterministic; equal to the two-step result up to that fp32
+    summation order); otherwise bitwise the two steps. x [M, K], weight [N, K], residual [M, N], all bf16."""
+    assert x.ndim == 2 and weight.ndim == 2 and x.shape[1] == weight.shape[1]
+    assert residual.shape == (x.shape[0], weight.shape[0]) and norm_w.shape == (weight.shape[0],)
+    K = x.shape[1]
+    ok = (x.dtype == weight.dtype == residual.dtype == norm_w.dtype == torch.bfloat16 and x.stride(1) == 1
+          and weight.stride(1) == 1 and K % 8 == 0 and x.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0
+          and residual.is_contiguous() and norm_w.is_contiguous()
+          and all(t.data_ptr() % 16 == 0 for t in (x, weight, residual, norm_w)))
+    if not ok:
+        from nanovllm_hip.kernels.rms_norm import fused_add_rms_norm
+        return fused_add_rms_norm(matmul(x, weight.t()), residual, norm_w, eps)
+    return torch.ops.nvhip.matmul_add_rms_norm(x, weight, residual, norm_w, float(eps))
+
+
 def add_rms_norm_matmul(x: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor, eps: float,
                         weight: torch.Tensor, silu: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """(matmul(RMSNorm(x + residual), weight.t()), x + residual) -- the product as matmul_silu_and_mul when silu --

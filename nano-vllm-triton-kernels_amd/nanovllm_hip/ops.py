@@ -25,6 +25,7 @@ _DEF.define("matmul(Tensor a, Tensor b, str input_precision) -> Tensor")
 _DEF.define("matmul_silu_mul(Tensor a, Tensor w) -> Tensor")
 _DEF.define("rms_norm_matmul(Tensor x, Tensor? residual, Tensor norm_w, float eps, Tensor w, bool silu) "
             "-> (Tensor, Tensor)")
+_DEF.define("matmul_add_rms_norm(Tensor x, Tensor w, Tensor residual, Tensor norm_w, float eps) -> (Tensor, Tensor)")
 _DEF.define("prefill_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
             "int max_seqlen_q, int max_seqlen_k, float scale, bool causal, Tensor? block_table) -> Tensor")
 _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
@@ -257,6 +258,32 @@ def _rms_norm_matmul_fake(x, residual, norm_w, eps, w, silu):
     N = w.shape[0] // 2 if silu else w.shape[0]
     out = torch.empty((x.shape[0], N), dtype=x.dtype, device=x.device)
     return out, (torch.empty_like(x) if residual is not None else x.new_empty((0,)))
+
+
+# ------------------------------------------------------------------ GEMM followed by the Add+RMSNorm that consumes it
+
+def _matmul_add_rms_norm_impl(x, w, residual, norm_w, eps):
+    M, K = x.shape
+    N = w.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    res_out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    lib = _lib.lib()
+    ws_bytes = lib.nvhip_matmul_add_rms_norm_workspace_size(M, N, K)
+    ws = torch.empty((max(ws_bytes, 16) + 3) // 4, dtype=torch.float32, device=x.device)
+    status = lib.nvhip_matmul_add_rms_norm_bf16(
+        y.data_ptr(), res_out.data_ptr(), x.data_ptr(), w.data_ptr(), residual.data_ptr(), norm_w.data_ptr(), eps,
+        M, N, K, x.stride(0), w.stride(0), ws.data_ptr(), ws.numel() * 4, _lib.stream_of(x))
+    _lib.check(status, "matmul_add_rms_norm")
+    return y, res_out
+
+
+_DEF.impl("matmul_add_rms_norm", _matmul_add_rms_norm_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::matmul_add_rms_norm")
+def _matmul_add_rms_norm_fake(x, w, residual, norm_w, eps):
+    out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+    return out, torch.empty_like(out)
 
 
 # ------------------------------------------------------------------ prefill (varlen) attention
