@@ -154,8 +154,8 @@ class Piecewise:
         for i in range(self.num_segments):
             if i:
                 q, k, v, _ = self.outs[(bucket, i - 1)]
-                self.o[:n] = self.model.attn(i - 1, q[:n], k[:n], v[:n], self.positions[:n], ctx, self.backend,
-                                             self.attention)
+                self.model.attn(i - 1, q[:n], k[:n], v[:n], self.positions[:n], ctx, self.backend, self.attention,
+                                out=self.o[:n])
             if self.graphs:
                 self.graphs[(bucket, i)].replay()
             else:

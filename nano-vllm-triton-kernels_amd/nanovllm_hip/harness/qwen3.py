@@ -256,9 +256,17 @@ class Qwen3:
             q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         return q, k, v, residual
 
-    def attn(self, li, q, k, v, positions, ctx: Context, backend, attention="torch"):
+    def attn(self, li, q, k, v, positions, ctx: Context, backend, attention="torch", out=None):
         """Attention.forward of layer li (layers/attention.py:64-92): the KV write (hip: the fused q/k norm + RoPE
-        + KV-write kernel) and the attention over the batch layout in ctx -> o [T, Hq, D]."""
+        + KV-write kernel) and the attention over the batch layout in ctx -> o [T, Hq, D], written into out when
+        given (the varlen hip attention writes it there directly; the other paths copy)."""
+        o = self._attn(li, q, k, v, positions, ctx, backend, attention, out)
+        if out is not None and o.data_ptr() != out.data_ptr():
+            out.copy_(o)
+            return out
+        return o
+
+    def _attn(self, li, q, k, v, positions, ctx: Context, backend, attention, out):
         c, L = self.cfg, self.layers[li]
         hq, D = c.num_attention_heads, c.head_dim
         k_cache, v_cache = self.kv[li]
@@ -273,7 +281,8 @@ class Qwen3:
             store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
         if varlen and attention == "hip":
             return flash_attn_varlen_func(q, k_cache, v_cache, ctx.max_seqlen_q, ctx.cu_seqlens_q, ctx.max_seqlen_k,
-                                          ctx.cu_seqlens_k, self.scale, causal=True, block_table=ctx.block_tables)
+                                          ctx.cu_seqlens_k, self.scale, causal=True, block_table=ctx.block_tables,
+                                          out=out)
         if varlen:
             return varlen_paged_attention(q, k_cache, v_cache, ctx.block_tables, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
                                           self.scale)

@@ -48,10 +48,12 @@ paged_decode_attention = flash_attn_with_kvcache
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
                            cu_seqlens_q: torch.Tensor, max_seqlen_k: int, cu_seqlens_k: torch.Tensor,
                            softmax_scale: float | None = None, causal: bool = False,
-                           block_table: torch.Tensor | None = None) -> torch.Tensor:
+                           block_table: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """q [Tq, Hq, D] bf16 -> o [Tq, Hq, D]. Without block_table k, v are [Tk, Hkv, D] (the new tokens' own keys);
     with it they are the paged caches [num_blocks, block_size, Hkv, D]. Query i of a sequence with lq queries and
-    lk keys sees keys j <= lk - lq + i when causal."""
+    lk keys sees keys j <= lk - lq + i when causal. out: an optional [Tq, Hq, D] bf16 tensor (dims contiguous,
+    8-byte aligned rows) the result is written into and returned -- an addition of this package, so that a caller
+    with a fixed output buffer (piecewise graphs) needs no copy."""
     assert q.dim() == 3 and q.dtype == torch.bfloat16 and q.stride(-1) == 1, (q.shape, q.dtype)
     Tq, Hq, D = q.shape
     assert k.dtype == v.dtype == torch.bfloat16 and k.shape == v.shape and k.shape[-1] == D
@@ -70,5 +72,11 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
     if q.stride(1) % 8 or q.stride(0) % 8:
         q = q.contiguous()
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    if out is not None:
+        assert out.shape == q.shape and out.dtype == torch.bfloat16 and out.stride(2) == 1, (out.shape, out.stride())
+        assert out.stride(1) % 4 == 0 and out.stride(0) % 4 == 0 and out.data_ptr() % 8 == 0
+        torch.ops.nvhip.prefill_attention_out(q, k, v, cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous(),
+                                              int(max_seqlen_q), int(max_seqlen_k), scale, causal, block_table, out)
+        return out
     return torch.ops.nvhip.prefill_attention(q, k, v, cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous(),
                                              int(max_seqlen_q), int(max_seqlen_k), scale, causal, block_table)

@@ -28,6 +28,9 @@ _DEF.define("rms_norm_matmul(Tensor x, Tensor? residual, Tensor norm_w, float ep
 _DEF.define("matmul_add_rms_norm(Tensor x, Tensor w, Tensor residual, Tensor norm_w, float eps) -> (Tensor, Tensor)")
 _DEF.define("prefill_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
             "int max_seqlen_q, int max_seqlen_k, float scale, bool causal, Tensor? block_table) -> Tensor")
+_DEF.define("prefill_attention_out(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
+            "int max_seqlen_q, int max_seqlen_k, float scale, bool causal, Tensor? block_table, "
+            "Tensor(a!) out) -> ()")
 _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
             "Tensor slot_mapping) -> ()")
 _DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
@@ -290,8 +293,16 @@ def _matmul_add_rms_norm_fake(x, w, residual, norm_w, eps):
 
 def _prefill_attention_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal,
                             block_table):
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _prefill_attention_out_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal,
+                                block_table, out)
+    return out
+
+
+def _prefill_attention_out_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal,
+                                block_table, out):
+    """Writes the attention into out [Tq, Hq, D] (rows of Hq * D contiguous heads: out.stride(2) == 1)."""
     Tq, Hq, D = q.shape
-    out = torch.empty((Tq, Hq, D), dtype=q.dtype, device=q.device)
     if block_table is None:
         Hkv, bt, bs, nb, mb = k.shape[1], None, 0, 0, 0
         k_st, v_st = k.stride(0), v.stride(0)
@@ -308,10 +319,10 @@ def _prefill_attention_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, m
         out.stride(1), bt, bs, nb, mb, scale, int(causal), ws.data_ptr() if ws is not None else None,
         ws_bytes if ws is not None else 0, _lib.stream_of(q))
     _lib.check(status, "prefill_attention")
-    return out
 
 
 _DEF.impl("prefill_attention", _prefill_attention_impl, "CUDA")
+_DEF.impl("prefill_attention_out", _prefill_attention_out_impl, "CUDA")
 
 
 @torch.library.register_fake("nvhip::prefill_attention")

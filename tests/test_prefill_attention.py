@@ -158,6 +158,21 @@ def test_few_decode_sequences_split_like_the_decode_call():
     assert torch.equal(out, dec.view(-1, 16, 128).cpu())
 
 
+def test_out_buffer_gets_the_same_rows():
+    """out= writes the result into a caller's buffer (a view of a larger one here) with the bits of the returned
+    tensor, for the prefill kernel's and the short-sequence path's rows."""
+    from nanovllm_hip.kernels.attention import flash_attn_varlen_func
+    lq, lk = [1, 40, 1, 3], [700, 300, 1500, 90]
+    q, kc, vc, bt = paged_case(lq, lk, 256, seed=14)
+    q, kc, vc, bt = q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV)
+    cq, ck = cu(lq).to(DEV), cu(lk).to(DEV)
+    want = flash_attn_varlen_func(q, kc, vc, max(lq), cq, max(lk), ck, 128 ** -0.5, True, bt)
+    buf = torch.full((q.shape[0] + 5, 16, 128), 7.0, dtype=torch.bfloat16, device=DEV)
+    got = flash_attn_varlen_func(q, kc, vc, max(lq), cq, max(lk), ck, 128 ** -0.5, True, bt, out=buf[2:2 + q.shape[0]])
+    assert got.data_ptr() == buf[2:].data_ptr() and torch.equal(got, want)
+    assert torch.all(buf[:2] == 7) and torch.all(buf[2 + q.shape[0]:] == 7)
+
+
 def test_chunk_over_a_long_prefix_splits_the_keys():
     """A 256-token chunk over 3840 cached keys: 16 blocks would stream 4096 keys each, so the call splits the keys
     into 16 ranges (256 blocks) and merges them (workspace query pinned on the CPU)."""
