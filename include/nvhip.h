@@ -219,6 +219,28 @@ int nvhip_matmul_add_rms_norm_bf16(void* y, void* residual_out, const void* x, c
 /* Bytes of workspace nvhip_matmul_add_rms_norm_bf16 needs for these sizes. Host-only, no GPU work. */
 int64_t nvhip_matmul_add_rms_norm_workspace_size(int64_t M, int64_t N, int64_t K);
 
+/*
+ * Decode with one token per sequence: nvhip_qk_norm_rope_kv_bf16 (q_out not written, no k_out) followed by
+ * nvhip_paged_decode_attention_bf16 (q_len 1, causal), in one launch. Not in the reference's kernels: its decode
+ * step runs qk_norm_rope_kv.py:92-125 and then flash_attn_with_kvcache (layers/attention.py:84-90) on the result.
+ * Each attention block (sequence b, kv head h) normalises and rotates its q rows with the arithmetic of the fused
+ * kernel (the same bits) and the block whose key range holds the new token (position context_lens[b] - 1) writes
+ * the new key (normed, rotated) and value of head h into slot slot_mapping[b] (skipped outside [0, num_blocks *
+ * block_size)) before it reads the cache; the output is bitwise that of the two calls.
+ *   q [num_seqs, Hq, D], k, v [num_seqs, Hkv, D]: the raw rows of the qkv projection (token strides q_stride,
+ *   k_stride, v_stride, multiples of 8; heads contiguous; 16-byte aligned). positions int64, slot_mapping int32
+ *   [num_seqs]; q_weight, k_weight [D]; cos_sin [max_pos, cos_sin_stride] fp32 (cos | sin); caches, block_table,
+ *   context_lens, out, scale and workspace (nvhip_paged_decode_attention_workspace_size with q_len 1) as for
+ *   nvhip_paged_decode_attention_bf16. D: 64 or 128; Hq / Hkv <= 16.
+ */
+int nvhip_qk_norm_rope_kv_decode_attention_bf16(
+    void* out, const void* q, const void* k, const void* v, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+    const int64_t* positions, const int32_t* slot_mapping, const void* q_weight, const void* k_weight,
+    const float* cos_sin, int64_t cos_sin_stride, int64_t max_pos, float eps, void* k_cache, void* v_cache,
+    const int32_t* block_table, const int32_t* context_lens, int64_t num_seqs, int64_t Hq, int64_t Hkv, int64_t D,
+    int64_t block_size, int64_t num_blocks, int64_t max_blocks, int64_t out_stride_token, int64_t out_stride_head,
+    float scale, void* workspace, int64_t workspace_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

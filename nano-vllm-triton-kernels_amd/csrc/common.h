@@ -136,6 +136,42 @@ __device__ __forceinline__ void store8(uint16_t* p, const u32x4& v) {
   }
 }
 
+// ---------------------------------------------------------------- device: per-head q/k RMSNorm + RoPE
+// The arithmetic of the fused q/k norm (qk_norm_rope_kv.hip) on the 8 + 8 elements one lane holds of a head row:
+// x1 = elements [e, e+8) of the first half, x2 = the same offsets of the second half (RoPE pairs x1[i], x2[i]).
+// Shared with the decode attention that applies it to its query rows, so both give the same bits.
+
+// This lane's part of the row's sum of squares (the row's lanes then sum their parts with group_sum).
+__device__ __forceinline__ float row_sumsq16(const float* x1, const float* x2) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ss = __builtin_fmaf(x1[i], x1[i], ss);
+    ss = __builtin_fmaf(x2[i], x2[i], ss);
+  }
+  return ss;
+}
+
+// n = bf16(bf16(x * rstd) * w), then y1 = bf16(n1 cos - n2 sin), y2 = bf16(n2 cos + n1 sin), every product rounded
+// on its own (w: the weights at the same offsets, c / s: cos and sin of the lane's 8 frequencies); elements 2j and
+// 2j+1 of each half share one packed bf16 conversion per rounding step.
+__device__ __forceinline__ void norm_rope16(const float* x1, const float* x2, float rstd, const u32x4& wa,
+                                            const u32x4& wb, const float* c, const float* s, u32x4& oa, u32x4& ob) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t n1 = pack_bf16x2(x1[2 * j] * rstd, x1[2 * j + 1] * rstd);  // bf16(x * rstd)
+    const uint32_t n2 = pack_bf16x2(x2[2 * j] * rstd, x2[2 * j + 1] * rstd);
+    const uint32_t m1 = pack_bf16x2(bf16_lo(n1) * bf16_lo(wa[j]), bf16_hi(n1) * bf16_hi(wa[j]));  // bf16(n * w)
+    const uint32_t m2 = pack_bf16x2(bf16_lo(n2) * bf16_lo(wb[j]), bf16_hi(n2) * bf16_hi(wb[j]));
+    const float a0 = bf16_lo(m1), a1 = bf16_hi(m1), b0 = bf16_lo(m2), b1 = bf16_hi(m2);
+    const int i0 = 2 * j, i1 = 2 * j + 1;
+    const float p0 = a0 * c[i0], q0 = b0 * s[i0], r0 = b0 * c[i0], u0 = a0 * s[i0];
+    const float p1 = a1 * c[i1], q1 = b1 * s[i1], r1 = b1 * c[i1], u1 = a1 * s[i1];
+    oa[j] = pack_bf16x2(p0 - q0, p1 - q1);
+    ob[j] = pack_bf16x2(r0 + u0, r1 + u1);
+  }
+}
+
 // ---------------------------------------------------------------- device: reductions
 
 // Sum over aligned groups of LANES consecutive lanes of a wave64 (LANES a power of two, 1..64). Every lane of a

@@ -71,6 +71,21 @@ struct DecodeArgs {
   // than q_len is left alone (the prefill kernel takes it). Null: q_len queries per sequence, ctx_lens.
   const int32_t* cu_q;
   const int32_t* cu_k;
+  // FUSE kernels (q_len 1, D 64 / 128): q, kn, vn are the raw rows of the qkv projection. The kernel applies the
+  // per-head RMSNorm + RoPE of qk_norm_rope_kv (common.h arithmetic, the same bits) to its query rows and to
+  // sequence b's new key; the block whose token range holds the new token (position ctx - 1) puts the new key and
+  // value row into LDS, uses them in place of what its chunk loads read for that token, and writes them into the
+  // cache slot slots[b] for the steps after this one.
+  const uint16_t* kn;
+  const uint16_t* vn;
+  int64_t kn_st, vn_st;
+  const int64_t* positions;
+  const int32_t* slots;
+  const uint16_t* q_w;
+  const uint16_t* k_w;
+  const float* cos_sin;
+  int64_t cs_st, max_pos, num_slots;
+  float inv_d, eps;
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -91,7 +106,7 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 }
 
 
-template <int D, int RP, bool ALIGNED>
+template <int D, int RP, bool ALIGNED, bool FUSE = false>
 __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const DecodeArgs g) {
   constexpr int NWV = block_waves(D);
   constexpr int KC = D / 32;         // 32-wide dim chunks of a K row (MFMA k steps of Q.K)
@@ -106,6 +121,8 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
   constexpr int VBYTES = NWV * kChunk * (VPW + KPW) * 2, RBYTES = NWV * RP * D * 4;
   __shared__ __attribute__((aligned(16))) unsigned char smem[VBYTES > RBYTES ? VBYTES : RBYTES];
   __shared__ float red_m[NWV][RP], red_l[NWV][RP];
+  __shared__ __attribute__((aligned(16))) uint16_t fresh[FUSE ? 2 * D : 8];  // FUSE: the new key and value rows
+  bool fresh_here = false;  // FUSE: this block's token range holds the new token (wave-uniform)
 
   const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
   const int b = pair / g.Hkv, kvh = pair % g.Hkv;
@@ -138,6 +155,84 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
   } else {
 #pragma unroll
     for (int c = 0; c < KC; ++c) qf[c] = bf16x8_t{};
+  }
+  if constexpr (FUSE) {
+    static_assert(D == 64 || D == 128, "fused pre-attention: head_dim 64 or 128");
+    const int64_t p = g.positions[b];
+    const float* cs = g.cos_sin + (p < 0 ? 0 : p >= g.max_pos ? g.max_pos - 1 : p) * g.cs_st;
+    // the query rows: lane group q8 / 8 = j0 holds the elements 8 j of the fused norm's lanes j = j0 + 4 u
+    // (chunk u of each half), so the sum of squares is rebuilt in that kernel's DPP order: lanes j ^ 1 and j ^ 2
+    // are lane groups 16 and 32 apart, and the last (mirror) step adds the two halves' partial sums
+    constexpr int HK = KC / 2;
+    float x1[HK][8], x2[HK][8], part[HK];
+#pragma unroll
+    for (int u = 0; u < HK; ++u) {
+      unpack8(__builtin_bit_cast(u32x4, qf[u]), x1[u]);
+      unpack8(__builtin_bit_cast(u32x4, qf[u + HK]), x2[u]);
+      part[u] = row_sumsq16(x1[u], x2[u]);
+      part[u] += __shfl_xor(part[u], 16);
+      part[u] += __shfl_xor(part[u], 32);
+    }
+    const float ss = HK == 1 ? part[0] : part[0] + part[HK - 1];
+    const float rstd = 1.0f / sqrtf(ss * g.inv_d + g.eps);
+#pragma unroll
+    for (int u = 0; u < HK; ++u) {
+      const int e = 32 * u + q8;
+      const u32x4 wa = *reinterpret_cast<const u32x4*>(g.q_w + e), wb = *reinterpret_cast<const u32x4*>(g.q_w + D / 2 + e);
+      float c[8], s[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = cs[e + i], s[i] = cs[D / 2 + e + i];
+      u32x4 oa, ob;
+      norm_rope16(x1[u], x2[u], rstd, wa, wb, c, s, oa, ob);
+      qf[u] = qrow < rows ? __builtin_bit_cast(bf16x8_t, oa) : bf16x8_t{};
+      qf[u + HK] = qrow < rows ? __builtin_bit_cast(bf16x8_t, ob) : bf16x8_t{};
+    }
+    // the new key (lanes 0 .. D/16-1 of wave 0, the fused norm's own lane layout) and value (the next D/16 lanes)
+    const int32_t slot = g.slots[b];
+    const bool writer = ctx > 0 ? (split * g.split_len <= ctx - 1 && ctx - 1 < split * g.split_len + g.split_len)
+                                : split == 0;
+    const bool store = writer && slot >= 0 && slot < g.num_slots;
+    // the new rows stand in for what the chunk loads read at position ctx - 1 when that is the slot they go to (a
+    // decode step); otherwise (inconsistent slot, clamped context) they are written before any wave reads
+    if (store && ctx > 0 && ctx == g.ctx_lens[b]) {
+      const int t = ctx - 1, blk = bt_row[t / g.bs];
+      fresh_here = blk >= 0 && int64_t(blk) * g.bs + t % g.bs == slot;
+    }
+    u32x4 na = {}, nb = {};  // this lane's 8 + 8 elements of the new key (lanes < D/16) or value row
+    constexpr int LN = D / 16;
+    const int e = 8 * (lane % LN);
+    if (store && wave == 0 && lane < D / 8) {
+      if (lane < LN) {
+        const uint16_t* kr = g.kn + int64_t(b) * g.kn_st + int64_t(kvh) * D;
+        float k1[8], k2[8];
+        unpack8(*reinterpret_cast<const u32x4*>(kr + e), k1);
+        unpack8(*reinterpret_cast<const u32x4*>(kr + D / 2 + e), k2);
+        const float kss = group_sum<LN>(row_sumsq16(k1, k2));
+        const float krstd = 1.0f / sqrtf(kss * g.inv_d + g.eps);
+        const u32x4 wa = *reinterpret_cast<const u32x4*>(g.k_w + e), wb = *reinterpret_cast<const u32x4*>(g.k_w + D / 2 + e);
+        float c[8], s[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = cs[e + i], s[i] = cs[D / 2 + e + i];
+        norm_rope16(k1, k2, krstd, wa, wb, c, s, na, nb);
+      } else {
+        const uint16_t* vr = g.vn + int64_t(b) * g.vn_st + int64_t(kvh) * D;
+        na = *reinterpret_cast<const u32x4*>(vr + e);
+        nb = *reinterpret_cast<const u32x4*>(vr + D / 2 + e);
+      }
+      uint16_t* f = fresh + (lane < LN ? 0 : D);
+      *reinterpret_cast<u32x4*>(f + e) = na;
+      *reinterpret_cast<u32x4*>(f + D / 2 + e) = nb;
+    }
+    uint16_t* dst = const_cast<uint16_t*>(lane < LN ? g.kc : g.vc) + int64_t(slot) * g.Hkv * D + int64_t(kvh) * D + e;
+    if (store && !fresh_here && wave == 0 && lane < D / 8) {
+      *reinterpret_cast<u32x4*>(dst) = na;
+      *reinterpret_cast<u32x4*>(dst + D / 2) = nb;
+    }
+    __syncthreads();  // the new rows are in LDS (or, without fresh_here, in the cache)
+    if (fresh_here && wave == 0 && lane < D / 8) {  // for the next steps; this kernel reads them from LDS
+      *reinterpret_cast<u32x4*>(dst) = na;
+      *reinterpret_cast<u32x4*>(dst + D / 2) = nb;
+    }
   }
   // row qrow sees tokens < row_limit
   const int row_limit = qrow >= rows ? 0 : g.causal ? min(max(ctx - lq + qi + 1, 0), ctx) : ctx;
@@ -192,6 +287,13 @@ __global__ __launch_bounds__(block_waves(D) * 64) void paged_decode_kernel(const
     for (int it = 0; it < PVI; ++it) {
       *reinterpret_cast<bf16x8_t*>(ks + (it * TPI + ts) * KPW + 8 * dg) = T.k[it];
       *reinterpret_cast<bf16x8_t*>(vs + (it * TPI + ts) * VPW + 8 * dg) = T.v[it];
+    }
+    if constexpr (FUSE) {  // the new token's rows from LDS: its cache slot is written only after this kernel read it
+      const int r = ctx - 1 - t0;
+      if (fresh_here && r >= 0 && r < kChunk && lane < D / 8) {
+        *reinterpret_cast<u32x4*>(ks + r * KPW + 8 * lane) = *reinterpret_cast<const u32x4*>(fresh + 8 * lane);
+        *reinterpret_cast<u32x4*>(vs + r * VPW + 8 * lane) = *reinterpret_cast<const u32x4*>(fresh + D + 8 * lane);
+      }
     }
     wave_sync();
     // scores: lane holds tokens t0 + 16u + 4 (l / 16) + r of row qrow
@@ -366,11 +468,11 @@ __global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) 
   }
 }
 
-template <int D, int RP>
+template <int D, int RP, bool FUSE = false>
 int launch_decode(const DecodeArgs& g, int64_t num_seqs, hipStream_t s) {
   const dim3 grid(unsigned(num_seqs * g.Hkv * g.splits)), block(block_waves(D) * 64);
-  if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true>), grid, block, 0, s, g);
-  else hipLaunchKernelGGL((paged_decode_kernel<D, RP, false>), grid, block, 0, s, g);
+  if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true, FUSE>), grid, block, 0, s, g);
+  else hipLaunchKernelGGL((paged_decode_kernel<D, RP, false, FUSE>), grid, block, 0, s, g);
   if (int rc = check_launch("paged_decode_attention")) return rc;
   if (g.splits == 1) return NVHIP_OK;
   hipLaunchKernelGGL((paged_decode_combine<D, RP>), dim3(unsigned(num_seqs * g.Hkv)), dim3(256), 0, s, g);
@@ -524,4 +626,76 @@ extern "C" int nvhip_paged_decode_attention_bf16(void* out, const void* q, const
     case 128: return launch_decode_rows<128>(g, num_seqs, int(rows), s);
     default: return launch_decode_rows<256>(g, num_seqs, int(rows), s);
   }
+}
+
+extern "C" int nvhip_qk_norm_rope_kv_decode_attention_bf16(
+    void* out, const void* q, const void* k, const void* v, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+    const int64_t* positions, const int32_t* slot_mapping, const void* q_weight, const void* k_weight,
+    const float* cos_sin, int64_t cos_sin_stride, int64_t max_pos, float eps, void* k_cache, void* v_cache,
+    const int32_t* block_table, const int32_t* context_lens, int64_t num_seqs, int64_t Hq, int64_t Hkv, int64_t D,
+    int64_t block_size, int64_t num_blocks, int64_t max_blocks, int64_t out_stride_token, int64_t out_stride_head,
+    float scale, void* workspace, int64_t workspace_size, void* stream) {
+  using namespace nvhip;
+  clear_error();
+  if (num_seqs < 0 || Hq < 1 || Hkv < 1 || block_size < 1 || num_blocks < 1 || max_blocks < 0)
+    return invalid("qk_norm_rope_kv_decode_attention: bad size");
+  if (Hq % Hkv != 0 || Hq / Hkv > 16)
+    return invalid("qk_norm_rope_kv_decode_attention: Hq must be a multiple of Hkv, at most 16 times it");
+  if (D != 64 && D != 128) return invalid("qk_norm_rope_kv_decode_attention: head_dim must be 64 or 128");
+  if (q_stride < Hq * D || k_stride < Hkv * D || v_stride < Hkv * D || q_stride % 8 || k_stride % 8 || v_stride % 8)
+    return invalid("qk_norm_rope_kv_decode_attention: bad q / k / v token strides");
+  if (out_stride_head < D || out_stride_token < Hq * out_stride_head)
+    return invalid("qk_norm_rope_kv_decode_attention: bad out strides");
+  if (max_pos <= 0 || cos_sin_stride < D || cos_sin_stride % 4)
+    return invalid("qk_norm_rope_kv_decode_attention: bad cos_sin cache shape");
+  if (num_seqs == 0) return NVHIP_OK;
+  if (!out || !q || !k || !v || !positions || !slot_mapping || !q_weight || !k_weight || !cos_sin || !k_cache ||
+      !v_cache || !block_table || !context_lens)
+    return invalid("qk_norm_rope_kv_decode_attention: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(q_weight) || !aligned16(k_weight) ||
+      !aligned16(cos_sin) || !aligned16(k_cache) || !aligned16(v_cache))
+    return invalid("qk_norm_rope_kv_decode_attention: q, k, v, weights, cos_sin and caches must be 16-byte aligned");
+  if (num_seqs * Hkv > INT32_MAX || max_blocks * block_size > INT32_MAX || num_blocks > INT32_MAX)
+    return invalid("qk_norm_rope_kv_decode_attention: size too large");
+  DecodeArgs g{};
+  g.out = static_cast<uint16_t*>(out);
+  g.q = static_cast<const uint16_t*>(q);
+  g.kc = static_cast<const uint16_t*>(k_cache);
+  g.vc = static_cast<const uint16_t*>(v_cache);
+  g.bt = block_table;
+  g.ctx_lens = context_lens;
+  g.q_len = 1, g.Hkv = int(Hkv), g.G = int(Hq / Hkv), g.bs = int(block_size), g.num_blocks = int(num_blocks);
+  g.max_blocks = int(max_blocks);
+  g.q_st = q_stride, g.q_sh = D, g.o_st = out_stride_token, g.o_sh = out_stride_head;
+  g.scale_log2 = scale * 1.4426950408889634f;
+  g.causal = 1;
+  g.splits = 1, g.split_len = int(max_blocks * block_size), g.ws = nullptr;
+  g.kn = static_cast<const uint16_t*>(k), g.vn = static_cast<const uint16_t*>(v);
+  g.kn_st = k_stride, g.vn_st = v_stride;
+  g.positions = positions, g.slots = slot_mapping;
+  g.q_w = static_cast<const uint16_t*>(q_weight), g.k_w = static_cast<const uint16_t*>(k_weight);
+  g.cos_sin = cos_sin, g.cs_st = cos_sin_stride, g.max_pos = max_pos, g.num_slots = num_blocks * block_size;
+  g.inv_d = 1.0f / float(D), g.eps = eps;
+  const int64_t need = workspace_bytes(num_seqs, 1, Hq, Hkv, D, max_blocks * block_size);
+  if (need > 0 && workspace && workspace_size >= need) {
+    if (reinterpret_cast<uintptr_t>(workspace) % alignof(float) != 0)
+      return invalid("qk_norm_rope_kv_decode_attention: workspace must be 4-byte aligned");
+    split_policy(num_seqs, Hkv, max_blocks * block_size, g.splits, g.split_len);
+    g.ws = static_cast<float*>(workspace);
+  }
+  if (num_seqs * Hkv * g.splits > INT32_MAX) return invalid("qk_norm_rope_kv_decode_attention: size too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rows = g.G;
+  if (D == 64) {
+    if (rows <= 1) return launch_decode<64, 1, true>(g, num_seqs, s);
+    if (rows <= 2) return launch_decode<64, 2, true>(g, num_seqs, s);
+    if (rows <= 4) return launch_decode<64, 4, true>(g, num_seqs, s);
+    if (rows <= 8) return launch_decode<64, 8, true>(g, num_seqs, s);
+    return launch_decode<64, 16, true>(g, num_seqs, s);
+  }
+  if (rows <= 1) return launch_decode<128, 1, true>(g, num_seqs, s);
+  if (rows <= 2) return launch_decode<128, 2, true>(g, num_seqs, s);
+  if (rows <= 4) return launch_decode<128, 4, true>(g, num_seqs, s);
+  if (rows <= 8) return launch_decode<128, 8, true>(g, num_seqs, s);
+  return launch_decode<128, 16, true>(g, num_seqs, s);
 }

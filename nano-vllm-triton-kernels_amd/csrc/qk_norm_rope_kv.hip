@@ -112,35 +112,14 @@ __device__ __forceinline__ void process_row(const QkArgs& a, int64_t t, int r, i
   }
 
   // sum of squares (fp32; the order and the fused multiply-adds differ from torch's reduction, within the
-  // rounding of one bf16 step of the normalised value)
+  // rounding of one bf16 step of the normalised value), then the norm and the rotation (common.h)
   float x1[8], x2[8];
   unpack8(xa, x1);
   unpack8(xb, x2);
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    ss = __builtin_fmaf(x1[i], x1[i], ss);
-    ss = __builtin_fmaf(x2[i], x2[i], ss);
-  }
-  ss = group_sum<D / 16>(ss);
+  const float ss = group_sum<D / 16>(row_sumsq16(x1, x2));
   const float rstd = 1.0f / sqrtf(ss * a.inv_d + a.eps);
-
-  // Elements 2j and 2j+1 of each half share one packed bf16 conversion per rounding step.
   u32x4 oa, ob;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t n1 = pack_bf16x2(x1[2 * j] * rstd, x1[2 * j + 1] * rstd);   // bf16(x * rstd)
-    const uint32_t n2 = pack_bf16x2(x2[2 * j] * rstd, x2[2 * j + 1] * rstd);
-    const uint32_t m1 = pack_bf16x2(bf16_lo(n1) * bf16_lo(wa[j]), bf16_hi(n1) * bf16_hi(wa[j]));  // bf16(n * w)
-    const uint32_t m2 = pack_bf16x2(bf16_lo(n2) * bf16_lo(wb[j]), bf16_hi(n2) * bf16_hi(wb[j]));
-    const float a0 = bf16_lo(m1), a1 = bf16_hi(m1), b0 = bf16_lo(m2), b1 = bf16_hi(m2);
-    const int i0 = 2 * j, i1 = 2 * j + 1;
-    // rotate: y1 = n1*cos - n2*sin, y2 = n2*cos + n1*sin, every product rounded on its own
-    const float p0 = a0 * c[i0], q0 = b0 * s[i0], r0 = b0 * c[i0], u0 = a0 * s[i0];
-    const float p1 = a1 * c[i1], q1 = b1 * s[i1], r1 = b1 * c[i1], u1 = a1 * s[i1];
-    oa[j] = pack_bf16x2(p0 - q0, p1 - q1);
-    ob[j] = pack_bf16x2(r0 + u0, r1 + u1);
-  }
+  norm_rope16(x1, x2, rstd, wa, wb, c, s, oa, ob);
 
   if (kind == 0) {
     uint16_t* dst = a.q_out + (t * a.Hq + h) * int64_t(D);

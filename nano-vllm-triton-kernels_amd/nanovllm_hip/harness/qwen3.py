@@ -25,7 +25,8 @@ import torch
 import torch.nn.functional as F
 
 from nanovllm_hip import kernels as hip
-from nanovllm_hip.kernels.attention import flash_attn_varlen_func, flash_attn_with_kvcache
+from nanovllm_hip.kernels.attention import (flash_attn_varlen_func, flash_attn_with_kvcache,
+                                            qk_norm_rope_kv_decode_attention)
 
 
 @dataclass
@@ -271,6 +272,11 @@ class Qwen3:
         hq, D = c.num_attention_heads, c.head_dim
         k_cache, v_cache = self.kv[li]
         varlen = ctx.is_prefill and ctx.block_tables is not None
+        if backend == "hip" and attention == "hip" and not ctx.is_prefill and q.shape[0] == ctx.context_lens.shape[0]:
+            # one decode token per sequence: the q/k norm + RoPE + KV write and the attention in one launch
+            return qk_norm_rope_kv_decode_attention(q, k, v, positions, L["q_norm"], L["k_norm"], c.rms_norm_eps,
+                                                    self.cos_sin, k_cache, v_cache, ctx.slot_mapping,
+                                                    ctx.context_lens, ctx.block_tables, self.scale)
         if backend == "hip":
             write_k = ctx.is_prefill and not varlen     # only a prefill without the cache reads k from here
             q, k_out = hip.qk_norm_rope_kv(q, k, v, positions, L["q_norm"], L["k_norm"], c.rms_norm_eps,

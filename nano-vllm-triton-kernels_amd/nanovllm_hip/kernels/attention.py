@@ -45,6 +45,41 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
 paged_decode_attention = flash_attn_with_kvcache
 
 
+def qk_norm_rope_kv_decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
+                                     q_weight: torch.Tensor, k_weight: torch.Tensor, eps: float,
+                                     cos_sin_cache: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                     slot_mapping: torch.Tensor, cache_seqlens: torch.Tensor,
+                                     block_table: torch.Tensor, softmax_scale: float | None = None) -> torch.Tensor:
+    """One decode token per sequence: qk_norm_rope_kv(q, k, v, ...) (writing the new k / v into the caches)
+    followed by flash_attn_with_kvcache(q_out, k_cache, v_cache, cache_seqlens, block_table, causal=True), in one
+    launch -> o [B, Hq, D]. q [B, Hq, D], k / v [B, Hkv, D] the raw (strided) views of the qkv projection, the other
+    arguments those of the two calls. The normed and rotated q / k are bitwise those of qk_norm_rope_kv and the
+    output that of the two-step sequence; q_out is not written. Falls back to the two calls for layouts the fused
+    kernel does not take (head_dim other than 64 / 128, unaligned rows, more than 16 q heads per kv head)."""
+    from nanovllm_hip.kernels.qk_norm_rope_kv import qk_norm_rope_kv
+    B, Hq, D = q.shape
+    Hkv = k.shape[1]
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1)
+    ok = (D in (64, 128) and Hq % Hkv == 0 and Hq // Hkv <= 16 and k.shape == v.shape == (B, Hkv, D)
+          and all(t.dtype == torch.bfloat16 and t.stride(2) == 1 and t.stride(1) == D and t.stride(0) % 8 == 0
+                  and t.data_ptr() % 16 == 0 for t in (q, k, v))
+          and q_weight.is_contiguous() and k_weight.is_contiguous() and q_weight.data_ptr() % 16 == 0
+          and k_weight.data_ptr() % 16 == 0 and cs.dtype == torch.float32 and cs.stride(1) == 1
+          and cs.shape[1] == D and cs.stride(0) % 4 == 0 and cs.data_ptr() % 16 == 0
+          and k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape[2:] == (Hkv, D)
+          and positions.dtype == torch.int64 and positions.shape == (B,) and slot_mapping.dtype == torch.int32
+          and slot_mapping.shape == (B,) and cache_seqlens.dtype == torch.int32 and block_table.dtype == torch.int32)
+    if not ok:
+        q_out, _ = qk_norm_rope_kv(q, k, v, positions, q_weight, k_weight, eps, cos_sin_cache, k_cache, v_cache,
+                                   slot_mapping, False)
+        return flash_attn_with_kvcache(q_out.view(B, 1, Hq, D), k_cache, v_cache, cache_seqlens, block_table, scale,
+                                       causal=True).view(B, Hq, D)
+    return torch.ops.nvhip.qk_norm_rope_kv_decode_attention(
+        q, k, v, positions.contiguous(), q_weight, k_weight, float(eps), cs, k_cache, v_cache,
+        slot_mapping.contiguous(), cache_seqlens.contiguous(), block_table.contiguous(), scale)
+
+
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
                            cu_seqlens_q: torch.Tensor, max_seqlen_k: int, cu_seqlens_k: torch.Tensor,
                            softmax_scale: float | None = None, causal: bool = False,

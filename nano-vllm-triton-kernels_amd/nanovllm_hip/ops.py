@@ -26,6 +26,9 @@ _DEF.define("matmul_silu_mul(Tensor a, Tensor w) -> Tensor")
 _DEF.define("rms_norm_matmul(Tensor x, Tensor? residual, Tensor norm_w, float eps, Tensor w, bool silu) "
             "-> (Tensor, Tensor)")
 _DEF.define("matmul_add_rms_norm(Tensor x, Tensor w, Tensor residual, Tensor norm_w, float eps) -> (Tensor, Tensor)")
+_DEF.define("qk_norm_rope_kv_decode_attention(Tensor q, Tensor k, Tensor v, Tensor positions, Tensor q_w, Tensor k_w, "
+            "float eps, Tensor cos_sin, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor slot_mapping, "
+            "Tensor cache_seqlens, Tensor block_table, float scale) -> Tensor")
 _DEF.define("prefill_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
             "int max_seqlen_q, int max_seqlen_k, float scale, bool causal, Tensor? block_table) -> Tensor")
 _DEF.define("prefill_attention_out(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
@@ -287,6 +290,37 @@ _DEF.impl("matmul_add_rms_norm", _matmul_add_rms_norm_impl, "CUDA")
 def _matmul_add_rms_norm_fake(x, w, residual, norm_w, eps):
     out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
     return out, torch.empty_like(out)
+
+
+# ------------------------------------------------------------------ fused q/k norm + RoPE + KV write + decode attention
+
+def _qk_norm_rope_kv_decode_attention_impl(q, k, v, positions, q_w, k_w, eps, cos_sin, k_cache, v_cache,
+                                           slot_mapping, cache_seqlens, block_table, scale):
+    B, Hq, D = q.shape
+    num_blocks, block_size, Hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    max_blocks = block_table.shape[1]
+    out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    lib = _lib.lib()
+    ws_bytes = lib.nvhip_paged_decode_attention_workspace_size(B, 1, Hq, Hkv, D, block_size, max_blocks)
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    cs = cos_sin.reshape(cos_sin.shape[0], -1)
+    status = lib.nvhip_qk_norm_rope_kv_decode_attention_bf16(
+        out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
+        positions.data_ptr(), slot_mapping.data_ptr(), q_w.data_ptr(), k_w.data_ptr(), cs.data_ptr(), cs.stride(0),
+        cs.shape[0], eps, k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(), cache_seqlens.data_ptr(),
+        B, Hq, Hkv, D, block_size, num_blocks, max_blocks, out.stride(0), out.stride(1), scale,
+        ws.data_ptr() if ws is not None else None, ws_bytes if ws is not None else 0, _lib.stream_of(q))
+    _lib.check(status, "qk_norm_rope_kv_decode_attention")
+    return out
+
+
+_DEF.impl("qk_norm_rope_kv_decode_attention", _qk_norm_rope_kv_decode_attention_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::qk_norm_rope_kv_decode_attention")
+def _qk_norm_rope_kv_decode_attention_fake(q, k, v, positions, q_w, k_w, eps, cos_sin, k_cache, v_cache,
+                                           slot_mapping, cache_seqlens, block_table, scale):
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
 
 # ------------------------------------------------------------------ prefill (varlen) attention
