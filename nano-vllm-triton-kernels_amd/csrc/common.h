@@ -23,6 +23,15 @@ int check_launch(const char* kernel);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// With defer_merge, paged_decode_varlen leaves the merge of its context splits to the caller's next kernel (the
+// prefill kernel of the same call, whose blocks for these sequences have nothing else to do) and describes the
+// records here: splits > 1, rows_padded (records per (sequence, kv head, split)), ws.
+struct DecodeSplits {
+  int splits = 1;
+  int rows_padded = 1;
+  const float* ws = nullptr;
+};
+
 // Paged attention over the sequences of a varlen call that have 1 .. qmax queries (qmax * Hq / Hkv <= 16), with the
 // paged decode kernel (paged_attention.hip): sequence b's queries are rows cu_q[b] .. cu_q[b+1]-1 of q / out, its
 // keys the first cu_k[b+1] - cu_k[b] tokens of block_table row b, causal aligned to the bottom right. Sequences
@@ -33,7 +42,7 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
                         const int32_t* block_table, const int32_t* cu_q, const int32_t* cu_k, int num_seqs, int qmax,
                         int Hq, int Hkv, int D, int block_size, int num_blocks, int max_blocks, int64_t q_st,
                         int64_t q_sh, int64_t o_st, int64_t o_sh, float scale, int causal, float* ws, int64_t ws_bytes,
-                        hipStream_t s);
+                        DecodeSplits* defer_merge, hipStream_t s);
 // Bytes of workspace paged_decode_varlen can use for num_seqs sequences of at most qmax queries (0: it never splits);
 // independent of the context lengths.
 int64_t paged_decode_varlen_workspace(int64_t num_seqs, int64_t qmax, int64_t Hq, int64_t Hkv, int64_t D);
@@ -170,6 +179,49 @@ __device__ __forceinline__ void norm_rope16(const float* x1, const float* x2, fl
     oa[j] = pack_bf16x2(p0 - q0, p1 - q1);
     ob[j] = pack_bf16x2(r0 + u0, r1 + u1);
   }
+}
+
+// ---------------------------------------------------------------- device: merging split attention records
+// Element d of row r of one (sequence, kv head) from its context splits' records (fp32 max, sum, two more, O[D] ...
+// at rec0 + s * step for split s, the (max, sum) pair first): O = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),
+// M = max_s m_s, merged in split order; 0 for a row no split saw (M = -inf). Up to 4 splits' loads issue at once.
+__device__ __forceinline__ float merge_splits(const float* rec0, int64_t step, int splits, int d_off) {
+  float num = 0.0f, den = 0.0f;
+  if (splits <= 4) {
+    float m[4], l[4], o[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      m[u] = -INFINITY, l[u] = o[u] = 0.0f;
+      if (u < splits) {
+        m[u] = rec0[u * step];
+        l[u] = rec0[u * step + 1];
+        o[u] = rec0[u * step + d_off];
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) M = fmaxf(M, m[u]);
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (u >= splits) break;
+        const float f = exp2f(m[u] - M);
+        num = __builtin_fmaf(o[u], f, num);
+        den = __builtin_fmaf(l[u], f, den);
+      }
+    }
+  } else {
+    float M = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, rec0[sp * step]);
+    if (M != -INFINITY) {
+      for (int sp = 0; sp < splits; ++sp) {
+        const float f = exp2f(rec0[sp * step] - M);
+        num = __builtin_fmaf(rec0[sp * step + d_off], f, num);
+        den = __builtin_fmaf(rec0[sp * step + 1], f, den);
+      }
+    }
+  }
+  return den > 0.0f ? num / den : 0.0f;
 }
 
 // ---------------------------------------------------------------- device: reductions

@@ -426,66 +426,30 @@ __global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) 
   for (int idx = threadIdx.x; idx < rows * D; idx += 256) {
     const int r = idx / D, d = idx % D;
     const float* rec = g.ws + (int64_t(pair) * g.splits * RP + r) * (2 + D);
-    const int64_t step = int64_t(RP) * (2 + D);
-    float num = 0.0f, den = 0.0f;
-    if (g.splits <= 4) {  // every load of the (max, sum, O) records issued at once
-      float m[4], l[4], o[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        m[u] = -INFINITY, l[u] = o[u] = 0.0f;
-        if (u < g.splits) {
-          m[u] = rec[u * step];
-          l[u] = rec[u * step + 1];
-          o[u] = rec[u * step + 2 + d];
-        }
-      }
-      float M = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) M = fmaxf(M, m[u]);
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (u >= g.splits) break;
-          const float f = exp2f(m[u] - M);
-          num = __builtin_fmaf(o[u], f, num);
-          den = __builtin_fmaf(l[u], f, den);
-        }
-      }
-    } else {
-      float M = -INFINITY;
-      for (int sp = 0; sp < g.splits; ++sp) M = fmaxf(M, rec[sp * step]);
-      if (M != -INFINITY) {
-        for (int sp = 0; sp < g.splits; ++sp) {
-          const float f = exp2f(rec[sp * step] - M);
-          num = __builtin_fmaf(rec[sp * step + 2 + d], f, num);
-          den = __builtin_fmaf(rec[sp * step + 1], f, den);
-        }
-      }
-    }
-    const float o = den > 0.0f ? num / den : 0.0f;
+    const float o = merge_splits(rec, int64_t(RP) * (2 + D), g.splits, 2 + d);
     const int i = r / g.G, hh = r % g.G;
     g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
   }
 }
 
 template <int D, int RP, bool FUSE = false>
-int launch_decode(const DecodeArgs& g, int64_t num_seqs, hipStream_t s) {
+int launch_decode(const DecodeArgs& g, int64_t num_seqs, hipStream_t s, bool merge = true) {
   const dim3 grid(unsigned(num_seqs * g.Hkv * g.splits)), block(block_waves(D) * 64);
   if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true, FUSE>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((paged_decode_kernel<D, RP, false, FUSE>), grid, block, 0, s, g);
   if (int rc = check_launch("paged_decode_attention")) return rc;
-  if (g.splits == 1) return NVHIP_OK;
+  if (g.splits == 1 || !merge) return NVHIP_OK;
   hipLaunchKernelGGL((paged_decode_combine<D, RP>), dim3(unsigned(num_seqs * g.Hkv)), dim3(256), 0, s, g);
   return check_launch("paged_decode_attention (combine)");
 }
 
 template <int D>
-int launch_decode_rows(const DecodeArgs& g, int64_t num_seqs, int rows, hipStream_t s) {
-  if (rows <= 1) return launch_decode<D, 1>(g, num_seqs, s);
-  if (rows <= 2) return launch_decode<D, 2>(g, num_seqs, s);
-  if (rows <= 4) return launch_decode<D, 4>(g, num_seqs, s);
-  if (rows <= 8) return launch_decode<D, 8>(g, num_seqs, s);
-  return launch_decode<D, 16>(g, num_seqs, s);
+int launch_decode_rows(const DecodeArgs& g, int64_t num_seqs, int rows, hipStream_t s, bool merge = true) {
+  if (rows <= 1) return launch_decode<D, 1>(g, num_seqs, s, merge);
+  if (rows <= 2) return launch_decode<D, 2>(g, num_seqs, s, merge);
+  if (rows <= 4) return launch_decode<D, 4>(g, num_seqs, s, merge);
+  if (rows <= 8) return launch_decode<D, 8>(g, num_seqs, s, merge);
+  return launch_decode<D, 16>(g, num_seqs, s, merge);
 }
 
 int rows_padded(int64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16; }
@@ -525,7 +489,7 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
                         const int32_t* block_table, const int32_t* cu_q, const int32_t* cu_k, int num_seqs, int qmax,
                         int Hq, int Hkv, int D, int block_size, int num_blocks, int max_blocks, int64_t q_st,
                         int64_t q_sh, int64_t o_st, int64_t o_sh, float scale, int causal, float* ws, int64_t ws_bytes,
-                        hipStream_t s) {
+                        DecodeSplits* defer_merge, hipStream_t s) {
   const int G = Hq / Hkv, rows = G * qmax;
   if (qmax < 1 || rows > 16 || (D != 64 && D != 128 && D != 256) ||
       int64_t(num_seqs) * Hkv > INT32_MAX || int64_t(max_blocks) * block_size > INT32_MAX)
@@ -544,10 +508,12 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
       g.ws = ws;
     }
   }
+  const bool merge = defer_merge == nullptr || g.splits == 1;
+  if (!merge) *defer_merge = DecodeSplits{g.splits, rows_padded(rows), g.ws};
   switch (D) {
-    case 64: return launch_decode_rows<64>(g, num_seqs, rows, s);
-    case 128: return launch_decode_rows<128>(g, num_seqs, rows, s);
-    default: return launch_decode_rows<256>(g, num_seqs, rows, s);
+    case 64: return launch_decode_rows<64>(g, num_seqs, rows, s, merge);
+    case 128: return launch_decode_rows<128>(g, num_seqs, rows, s, merge);
+    default: return launch_decode_rows<256>(g, num_seqs, rows, s, merge);
   }
 }
 

@@ -67,6 +67,10 @@ struct PrefillArgs {
   int Hq;
   int64_t ws_rows;  // Tq: query rows of one split's records
   float* ws;        // splits > 1: [splits, Tq, Hq, D + 4] fp32 records (max, sum, -, -, O) merged by prefill_combine
+  // the paged decode kernel's context splits of the short sequences (dec_splits > 1), merged here by blocks that
+  // have no queries of their own: records [num_seqs, Hkv, dec_splits, dec_rp, 2 + D]
+  int dec_splits, dec_rp;
+  const float* dec_ws;
 };
 
 // fp32 elements of one (split, query, head) record: max, row sum, two unused (16-byte aligned O), O[D].
@@ -119,7 +123,20 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   const int h = hg * HB + int(threadIdx.x) / kHeadThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
-  if (lq >= 1 && lq <= g.lq_skip) return;  // the whole block: b is uniform
+  if (lq >= 1 && lq <= g.lq_skip) {  // the paged decode kernel took this sequence (the whole block: b is uniform)
+    // one block per (sequence, kv head) merges that kernel's context splits, as paged_decode_combine would
+    if (g.dec_splits > 1 && ci == 0 && (hg * HB) % g.G == 0) {
+      const int kvm = hg * HB / g.G, rows = g.G * lq;
+      const int64_t pair = int64_t(b) * g.Hkv + kvm, step = int64_t(g.dec_rp) * (2 + D);
+      for (int idx = threadIdx.x; idx < rows * D; idx += kThreads) {
+        const int r = idx / D, d = idx % D;
+        const float o = merge_splits(g.dec_ws + (pair * g.dec_splits * g.dec_rp + r) * (2 + D), step, g.dec_splits,
+                                     2 + d);
+        g.out[int64_t(q0s + r / g.G) * g.o_st + int64_t(kvm * g.G + r % g.G) * g.o_sh + d] = f32_to_bf16(o);
+      }
+    }
+    return;
+  }
   // keys [k_beg, k_stop) of this block: the split's range, cut at the last key its query tile sees
   const int k_beg = split * g.split_len;
   const int k_hi = split == g.splits - 1 ? INT32_MAX : k_beg + g.split_len;  // the last split takes the rest
@@ -586,13 +603,17 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
     const int64_t off = decode_workspace_offset(need);
     float* dws = workspace && workspace_size > off ? reinterpret_cast<float*>(static_cast<char*>(workspace) + off)
                                                    : nullptr;
+    // the prefill kernel, launched next when some sequence has more queries, merges the decode splits
+    DecodeSplits dsplit;
+    const bool defer = max_seqlen_q > g.lq_skip;
     if (int rc = paged_decode_varlen(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(q),
                                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), block_table,
                                      cu_seqlens_q, cu_seqlens_k, int(num_seqs), g.lq_skip, int(Hq), int(Hkv), int(D),
                                      int(block_size), int(num_blocks), int(max_blocks), q_stride_token,
                                      q_stride_head, out_stride_token, out_stride_head, scale, causal, dws,
-                                     dws ? workspace_size - off : 0, s))
+                                     dws ? workspace_size - off : 0, defer ? &dsplit : nullptr, s))
       return rc;
+    g.dec_splits = dsplit.splits, g.dec_rp = dsplit.rows_padded, g.dec_ws = dsplit.ws;
     if (max_seqlen_q <= g.lq_skip) return NVHIP_OK;
   }
 #define NVHIP_PREFILL_LAUNCH(DD, PG, HBV) hipLaunchKernelGGL((prefill_attention_kernel<DD, PG, HBV>), grid, block, 0, s, g)
