@@ -23,17 +23,9 @@ int check_launch(const char* kernel);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// With defer_merge, paged_decode_varlen leaves the merge of its context splits to the caller's next kernel (the
-// prefill kernel of the same call, whose blocks for these sequences have nothing else to do) and describes the
-// records here: splits > 1, rows_padded (records per (sequence, kv head, split)), ws.
-struct DecodeSplits {
-  int splits = 1;
-  int rows_padded = 1;
-  const float* ws = nullptr;
-};
-
 // Paged attention over the sequences of a varlen call that have 1 .. qmax queries (qmax * Hq / Hkv <= 16), with the
-// paged decode kernel (paged_attention.hip): sequence b's queries are rows cu_q[b] .. cu_q[b+1]-1 of q / out, its
+// paged decode kernel (paged_attention.hip), for a call with no longer sequence (otherwise the prefill kernel's
+// blocks of these sequences run the same decode body, decode_attention.h): sequence b's queries are rows cu_q[b] .. cu_q[b+1]-1 of q / out, its
 // keys the first cu_k[b+1] - cu_k[b] tokens of block_table row b, causal aligned to the bottom right. Sequences
 // with more queries are not touched. With a workspace of at least paged_decode_varlen_workspace(...) bytes the keys
 // of each (sequence, kv head) are split over blocks when there are fewer pairs than CUs (as the decode entry point
@@ -42,7 +34,7 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
                         const int32_t* block_table, const int32_t* cu_q, const int32_t* cu_k, int num_seqs, int qmax,
                         int Hq, int Hkv, int D, int block_size, int num_blocks, int max_blocks, int64_t q_st,
                         int64_t q_sh, int64_t o_st, int64_t o_sh, float scale, int causal, float* ws, int64_t ws_bytes,
-                        DecodeSplits* defer_merge, hipStream_t s);
+                        hipStream_t s);
 // Bytes of workspace paged_decode_varlen can use for num_seqs sequences of at most qmax queries (0: it never splits);
 // independent of the context lengths.
 int64_t paged_decode_varlen_workspace(int64_t num_seqs, int64_t qmax, int64_t Hq, int64_t Hkv, int64_t D);

@@ -33,7 +33,7 @@
 // (max, sum, O) records and prefill_combine merges them in split order.
 #include <algorithm>
 
-#include "common.h"
+#include "decode_attention.h"
 
 namespace nvhip {
 namespace {
@@ -67,10 +67,11 @@ struct PrefillArgs {
   int Hq;
   int64_t ws_rows;  // Tq: query rows of one split's records
   float* ws;        // splits > 1: [splits, Tq, Hq, D + 4] fp32 records (max, sum, -, -, O) merged by prefill_combine
-  // the paged decode kernel's context splits of the short sequences (dec_splits > 1), merged here by blocks that
-  // have no queries of their own: records [num_seqs, Hkv, dec_splits, dec_rp, 2 + D]
-  int dec_splits, dec_rp;
-  const float* dec_ws;
+  // dec_inline: the blocks of the short sequences (1 .. lq_skip queries) run their paged decode attention
+  // themselves (one block per (sequence, kv head), dec: its varlen arguments, one split), concurrently with the
+  // prefill tiles, instead of a separate launch before this one
+  int dec_inline;
+  DecodeArgs dec;
 };
 
 // fp32 elements of one (split, query, head) record: max, row sum, two unused (16-byte aligned O), O[D].
@@ -97,7 +98,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // half-wave (4 keys x 32 dims) hit 64 distinct banks
   constexpr int VP = D + 32;
   constexpr int STAGE = kBK * (KP + VP);  // elements of one LDS stage (K tile, then V tile)
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  // LDS: two K/V tile stages, or (paged) the decode attention's buffers for the blocks of short sequences
+  constexpr int DEC_BYTES = PAGED ? decode_lds_bytes(D, 16, false) : 0;
+  constexpr int LDS_ELEMS = (2 * STAGE * 2 > DEC_BYTES ? 2 * STAGE * 2 : DEC_BYTES) / 2;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
 
   // Block order. The ids are dealt round-robin over the 8 XCDs (block b runs on XCD b % 8) and each XCD starts its
   // blocks in id order as CUs free up. When the groups (sequence, head group) divide evenly, XCD x takes whole
@@ -123,16 +127,13 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   const int h = hg * HB + int(threadIdx.x) / kHeadThreads, kvh = (hg * HB) / g.G;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   const int k0s = g.cu_k[b], lk = g.cu_k[b + 1] - k0s;
-  if (lq >= 1 && lq <= g.lq_skip) {  // the paged decode kernel took this sequence (the whole block: b is uniform)
-    // one block per (sequence, kv head) merges that kernel's context splits, as paged_decode_combine would
-    if (g.dec_splits > 1 && ci == 0 && (hg * HB) % g.G == 0) {
-      const int kvm = hg * HB / g.G, rows = g.G * lq;
-      const int64_t pair = int64_t(b) * g.Hkv + kvm, step = int64_t(g.dec_rp) * (2 + D);
-      for (int idx = threadIdx.x; idx < rows * D; idx += kThreads) {
-        const int r = idx / D, d = idx % D;
-        const float o = merge_splits(g.dec_ws + (pair * g.dec_splits * g.dec_rp + r) * (2 + D), step, g.dec_splits,
-                                     2 + d);
-        g.out[int64_t(q0s + r / g.G) * g.o_st + int64_t(kvm * g.G + r % g.G) * g.o_sh + d] = f32_to_bf16(o);
+  if (lq >= 1 && lq <= g.lq_skip) {  // the paged decode attention takes this sequence (the whole block: b is uniform)
+    // one block per (sequence, kv head) runs the decode attention of the pair (the whole block: b, hg, ci uniform)
+    if constexpr (PAGED) {
+      if (g.dec_inline && ci == 0 && (hg * HB) % g.G == 0) {
+        const int pair = b * g.Hkv + hg * HB / g.G;
+        if (g.dec.bs % 32 == 0) decode_block<D, 16, true>(g.dec, pair, reinterpret_cast<unsigned char*>(lds));
+        else decode_block<D, 16, false>(g.dec, pair, reinterpret_cast<unsigned char*>(lds));
       }
     }
     return;
@@ -603,18 +604,30 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
     const int64_t off = decode_workspace_offset(need);
     float* dws = workspace && workspace_size > off ? reinterpret_cast<float*>(static_cast<char*>(workspace) + off)
                                                    : nullptr;
-    // the prefill kernel, launched next when some sequence has more queries, merges the decode splits
-    DecodeSplits dsplit;
-    const bool defer = max_seqlen_q > g.lq_skip;
-    if (int rc = paged_decode_varlen(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(q),
-                                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), block_table,
-                                     cu_seqlens_q, cu_seqlens_k, int(num_seqs), g.lq_skip, int(Hq), int(Hkv), int(D),
-                                     int(block_size), int(num_blocks), int(max_blocks), q_stride_token,
-                                     q_stride_head, out_stride_token, out_stride_head, scale, causal, dws,
-                                     dws ? workspace_size - off : 0, defer ? &dsplit : nullptr, s))
-      return rc;
-    g.dec_splits = dsplit.splits, g.dec_rp = dsplit.rows_padded, g.dec_ws = dsplit.ws;
-    if (max_seqlen_q <= g.lq_skip) return NVHIP_OK;
+    // When some sequence has more queries the prefill kernel is launched and its blocks of the short sequences run
+    // their decode attention (unsplit) alongside the prefill tiles; otherwise the decode kernel runs alone, its
+    // contexts split over blocks with the workspace
+    const int64_t G = Hq / Hkv;
+    if (max_seqlen_q > g.lq_skip && G * g.lq_skip <= 16) {
+      DecodeArgs& d = g.dec;
+      d.out = static_cast<uint16_t*>(out), d.q = static_cast<const uint16_t*>(q);
+      d.kc = static_cast<const uint16_t*>(k), d.vc = static_cast<const uint16_t*>(v), d.bt = block_table;
+      d.q_len = g.lq_skip, d.Hkv = int(Hkv), d.G = int(G), d.bs = int(block_size), d.num_blocks = int(num_blocks);
+      d.max_blocks = int(max_blocks);
+      d.q_st = q_stride_token, d.q_sh = q_stride_head, d.o_st = out_stride_token, d.o_sh = out_stride_head;
+      d.scale_log2 = scale * 1.4426950408889634f, d.causal = causal ? 1 : 0;
+      d.splits = 1, d.split_len = int(max_blocks * block_size);
+      d.cu_q = cu_seqlens_q, d.cu_k = cu_seqlens_k;
+      g.dec_inline = 1;
+    }
+    if (!g.dec_inline) {
+      return paged_decode_varlen(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(q),
+                                 static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), block_table,
+                                 cu_seqlens_q, cu_seqlens_k, int(num_seqs), g.lq_skip, int(Hq), int(Hkv), int(D),
+                                 int(block_size), int(num_blocks), int(max_blocks), q_stride_token, q_stride_head,
+                                 out_stride_token, out_stride_head, scale, causal, dws,
+                                 dws ? workspace_size - off : 0, s);
+    }
   }
 #define NVHIP_PREFILL_LAUNCH(DD, PG, HBV) hipLaunchKernelGGL((prefill_attention_kernel<DD, PG, HBV>), grid, block, 0, s, g)
   if (hb == 2 && D == 64 && paged) NVHIP_PREFILL_LAUNCH(64, true, 2);
