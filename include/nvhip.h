@@ -169,9 +169,9 @@ int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_ca
  *   workspace: device memory of at least nvhip_prefill_attention_workspace_size(...) bytes, 16-byte aligned
  *   (contents need no initialisation), or NULL / too small: then the keys of a sequence are never split over
  *   blocks. With it, few query tiles over long key ranges (a prompt chunk over its cached prefix) are spread over
- *   the CUs in key ranges whose partial results a second kernel merges, and, with a block table, the short
- *   sequences' contexts are split as nvhip_paged_decode_attention_bf16 splits them (fewer (sequence, kv head)
- *   pairs than CUs). Calls that share a workspace must be ordered on one stream.
+ *   the CUs in key ranges whose partial results a second kernel merges, and, with a block table and only short
+ *   sequences, their contexts are split as nvhip_paged_decode_attention_bf16 splits them (fewer (sequence, kv
+ *   head) pairs than CUs). Calls that share a workspace must be ordered on one stream.
  * Numerics: fp32 scores and online softmax, P rounded to bf16 for P.V (as flash-attn), fp32 accumulation, bf16 out.
  */
 int nvhip_prefill_attention_bf16(void* out, const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
