@@ -39,9 +39,9 @@ struct DecodeArgs {
   const int32_t* cu_k;
   // FUSE kernels (q_len 1, D 64 / 128): q, kn, vn are the raw rows of the qkv projection. The kernel applies the
   // per-head RMSNorm + RoPE of qk_norm_rope_kv (common.h arithmetic, the same bits) to its query rows and to
-  // sequence b's new key; the block whose token range holds the new token (position ctx - 1) puts the new key and
-  // value row into LDS, uses them in place of what its chunk loads read for that token, and writes them into the
-  // cache slot slots[b] for the steps after this one.
+  // sequence b's new key; in the block whose token range holds the new token (position ctx - 1) the wave whose
+  // chunk holds it computes the new key and value rows, uses them in place of what its chunk load read for that
+  // token, and writes them into the cache slot slots[b] for the steps after this one.
   const uint16_t* kn;
   const uint16_t* vn;
   int64_t kn_st, vn_st;
@@ -72,11 +72,11 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 }
 
 
-// Bytes of LDS decode_block uses: every wave's K and V chunk (or, afterwards, its partial O), the waves' row max and
-// sum, and (FUSE) the new key and value rows.
-__host__ __device__ constexpr int decode_lds_bytes(int D, int RP, bool FUSE) {
+// Bytes of LDS decode_block uses: every wave's K and V chunk (or, afterwards, its partial O) and the waves' row max
+// and sum.
+__host__ __device__ constexpr int decode_lds_bytes(int D, int RP, bool) {
   const int nwv = D == 256 ? 4 : 8, vb = nwv * 32 * ((D + 16) + (D + 8)) * 2, rb = nwv * RP * D * 4;
-  return (vb > rb ? vb : rb) + 2 * nwv * RP * 4 + (FUSE ? 4 * D : 16);
+  return (vb > rb ? vb : rb) + 2 * nwv * RP * 4;
 }
 
 template <int D, int RP, bool ALIGNED, bool FUSE = false>
@@ -92,13 +92,13 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
   static_assert(D % 32 == 0 && D <= 256 && RP <= 16, "shape");
   // LDS: each wave's K and V chunks during the loop, the waves' partial O afterwards (same bytes)
   constexpr int VBYTES = NWV * kChunk * (VPW + KPW) * 2, RBYTES = NWV * RP * D * 4;
-  static_assert(decode_lds_bytes(D, RP, FUSE) == (VBYTES > RBYTES ? VBYTES : RBYTES) + 2 * NWV * RP * 4 +
-                    (FUSE ? 4 * D : 16), "LDS layout");
+  static_assert(decode_lds_bytes(D, RP, FUSE) == (VBYTES > RBYTES ? VBYTES : RBYTES) + 2 * NWV * RP * 4,
+                "LDS layout");
   unsigned char* smem = lds;  // the waves' K / V chunks, then their partial O
   float (*red_m)[RP] = reinterpret_cast<float (*)[RP]>(lds + (VBYTES > RBYTES ? VBYTES : RBYTES));
   float (*red_l)[RP] = red_m + NWV;
-  uint16_t* fresh = reinterpret_cast<uint16_t*>(red_l + NWV);  // FUSE: the new key and value rows
   bool fresh_here = false;  // FUSE: this block's token range holds the new token (wave-uniform)
+  u32x4 na = {}, nb = {};    // FUSE: this lane's 8 + 8 elements of the new key (lanes < D/16) or value row
 
   const int split = bid % g.splits, pair = bid / g.splits;
   const int b = pair / g.Hkv, kvh = pair % g.Hkv;
@@ -174,10 +174,12 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
       const int t = ctx - 1, blk = bt_row[t / g.bs];
       fresh_here = blk >= 0 && int64_t(blk) * g.bs + t % g.bs == slot;
     }
-    u32x4 na = {}, nb = {};  // this lane's 8 + 8 elements of the new key (lanes < D/16) or value row
+    // computed by the wave whose chunk holds the new token (no block barrier), or by wave 0 when they must reach the
+    // cache before any wave reads it
     constexpr int LN = D / 16;
     const int e = 8 * (lane % LN);
-    if (store && wave == 0 && lane < D / 8) {
+    const int cw = fresh_here ? ((ctx - 1) / kChunk - tok_begin / kChunk) % NWV : 0;
+    if (store && wave == cw && lane < D / 8) {
       if (lane < LN) {
         const uint16_t* kr = g.kn + int64_t(b) * g.kn_st + int64_t(kvh) * D;
         float k1[8], k2[8];
@@ -195,20 +197,13 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
         na = *reinterpret_cast<const u32x4*>(vr + e);
         nb = *reinterpret_cast<const u32x4*>(vr + D / 2 + e);
       }
-      uint16_t* f = fresh + (lane < LN ? 0 : D);
-      *reinterpret_cast<u32x4*>(f + e) = na;
-      *reinterpret_cast<u32x4*>(f + D / 2 + e) = nb;
-    }
-    uint16_t* dst = const_cast<uint16_t*>(lane < LN ? g.kc : g.vc) + int64_t(slot) * g.Hkv * D + int64_t(kvh) * D + e;
-    if (store && !fresh_here && wave == 0 && lane < D / 8) {
+      // into the cache for the next steps (with fresh_here this kernel takes them from the registers instead)
+      uint16_t* dst = const_cast<uint16_t*>(lane < LN ? g.kc : g.vc) + int64_t(slot) * g.Hkv * D +
+                      int64_t(kvh) * D + e;
       *reinterpret_cast<u32x4*>(dst) = na;
       *reinterpret_cast<u32x4*>(dst + D / 2) = nb;
     }
-    __syncthreads();  // the new rows are in LDS (or, without fresh_here, in the cache)
-    if (fresh_here && wave == 0 && lane < D / 8) {  // for the next steps; this kernel reads them from LDS
-      *reinterpret_cast<u32x4*>(dst) = na;
-      *reinterpret_cast<u32x4*>(dst + D / 2) = nb;
-    }
+    if (store && !fresh_here) __syncthreads();  // block-uniform: the rows are in the cache before any wave reads
   }
   // row qrow sees tokens < row_limit
   const int row_limit = qrow >= rows ? 0 : g.causal ? min(max(ctx - lq + qi + 1, 0), ctx) : ctx;
@@ -264,11 +259,14 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
       *reinterpret_cast<bf16x8_t*>(ks + (it * TPI + ts) * KPW + 8 * dg) = T.k[it];
       *reinterpret_cast<bf16x8_t*>(vs + (it * TPI + ts) * VPW + 8 * dg) = T.v[it];
     }
-    if constexpr (FUSE) {  // the new token's rows from LDS: its cache slot is written only after this kernel read it
+    if constexpr (FUSE) {  // the new token's rows from the registers of this wave (the only one with its chunk)
       const int r = ctx - 1 - t0;
       if (fresh_here && r >= 0 && r < kChunk && lane < D / 8) {
-        *reinterpret_cast<u32x4*>(ks + r * KPW + 8 * lane) = *reinterpret_cast<const u32x4*>(fresh + 8 * lane);
-        *reinterpret_cast<u32x4*>(vs + r * VPW + 8 * lane) = *reinterpret_cast<const u32x4*>(fresh + D + 8 * lane);
+        constexpr int LN = D / 16;
+        uint16_t* row = lane < LN ? ks + r * KPW : vs + r * VPW;
+        const int e = 8 * (lane % LN);
+        *reinterpret_cast<u32x4*>(row + e) = na;
+        *reinterpret_cast<u32x4*>(row + D / 2 + e) = nb;
       }
     }
     wave_sync();
