@@ -137,20 +137,105 @@ __device__ __forceinline__ void store8(uint16_t* p, const u32x4& v) {
   }
 }
 
+// ---------------------------------------------------------------- RMSNorm in torch's GPU order
+// The reference's RMSNorm (layers/layernorm.py:20-44) run eagerly on the GPU computes mean(x^2) with ATen's generic
+// reduction and rsqrt with ATen's rsqrt kernel. The kernels here reproduce both bit for bit:
+//  - torch.rsqrt on a float tensor evaluates the double-precision device rsqrt and rounds it to float;
+//  - the mean is an fp32 sum in ATen's order times factor = float(rows) / float(rows * n) (fp32), where the order
+//    depends on n and on the number of rows: block width bw (threads per row) from aten_norm_bw(); thread L of a
+//    row sums the 4-element vectors L, L + bw, ... (n >= 128; one accumulator per vector component, each from 0,
+//    combined as ((a0 + a1) + a2) + a3), or single elements (n < 128); then for bw > 64 t[L] += t[L + off] for
+//    off = bw/2 .. 64, then a tree of adjacent lanes (t[L] += t[L + 1], t[L] += t[L + 2], ...).
+// A butterfly (xor) reduction gives every lane the value lane 0 of that tree gets (each level adds the same two
+// operands), so group_sum below finishes it once each lane holds the partial of adjacent thread(s).
+
+// (float) rsqrt((double) v): torch.rsqrt's result on a float tensor (its kernel calls the double overload).
+__device__ __forceinline__ float torch_rsqrt(float v) { return float(rsqrt(double(v))); }
+
+// ATen's threads per row (bw) for the mean over rows of n fp32 values, or 0 when a row is split over the waves of
+// a block (then the order is not the one described above). Host-side; a restatement of the launch-shape
+// arithmetic of torch's GPU reduction for a contiguous innermost dimension.
+inline int aten_norm_bw(int64_t n, int64_t rows) {
+  auto last_pow2 = [](int64_t x) { int64_t p = 1; while (p * 2 <= x) p *= 2; return p; };
+  const int64_t dim0 = n >= 128 ? n / 4 : n;
+  const int64_t d0 = dim0 < 512 ? last_pow2(dim0) : 512, d1 = rows < 512 ? last_pow2(rows) : 512;
+  int64_t bw = d0 < 64 ? d0 : 64;
+  const int64_t bh = d1 < 512 / bw ? d1 : 512 / bw;
+  bw = d0 < 512 / bh ? d0 : 512 / bh;
+  const int64_t per_thread = (n + bw - 1) / bw, split_at = bh * 16 < 256 ? bh * 16 : 256;
+  if (bh > 1 && per_thread >= split_at) return 0;
+  return int(bw);
+}
+// MeanOps' factor: float(num_outputs) / numel with the int64 numel converted to float.
+inline float aten_mean_factor(int64_t n, int64_t rows) { return float(rows) / float(rows * n); }
+
+// Thread partial over one 4-element vector of squares: ((y0 + y1) + y2) + y3.
+__device__ __forceinline__ float sumsq4(const float* x) {
+  return ((x[0] * x[0] + x[1] * x[1]) + x[2] * x[2]) + x[3] * x[3];
+}
+
+// Row layout "T32" for rows of n = 256 K elements (or 128, K = 1, with 16 lanes): a row is owned by 32 aligned
+// lanes, lane j holding the 16-byte chunks k = 0 .. K-1 at elements 8 j + 256 k, i.e. the 4-element vectors
+// 2 j + 64 k and 2 j + 1 + 64 k. With bw = 64 M, ATen thread 2 j + p + 64 c (p = 0, 1; c < M) owns exactly the
+// vectors of chunks c, c + M, c + 2M, ... of parity p, so every thread partial and the bw > 64 halving levels are
+// local to lane j, which returns t[2j] + t[2j+1] of the 64-wide tree (the first in-wave level). v[k][e]: element
+// e of chunk k (fp32; the squares are formed here, each rounded). group_sum<32> then completes the sum.
+template <int K, int M>
+__device__ __forceinline__ float t32_partial(const float (*v)[8]) {
+  static_assert(M >= 1 && M <= 8 && (M & (M - 1)) == 0 && M <= K, "bw = 64 M with M <= K");
+  float t[2][M];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int c = 0; c < M; ++c) {
+      float acc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = v[c][4 * p + i] * v[c][4 * p + i];
+#pragma unroll
+      for (int k = c + M; k < K; k += M)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += v[k][4 * p + i] * v[k][4 * p + i];
+      t[p][c] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    }
+#pragma unroll
+  for (int off = M / 2; off >= 1; off /= 2)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int c = 0; c < off; ++c) t[p][c] += t[p][c + off];
+  return t[0][0] + t[1][0];
+}
+
+// t32_partial for a runtime M (wave-uniform): bw / 64 of the call, 1 .. min(8, K), a power of two.
+template <int K>
+__device__ __forceinline__ float t32_partial_m(const float (*v)[8], int m) {
+  if constexpr (K >= 8)
+    if (m >= 8) return t32_partial<K, 8>(v);
+  if constexpr (K >= 4)
+    if (m >= 4) return t32_partial<K, 4>(v);
+  if constexpr (K >= 2)
+    if (m >= 2) return t32_partial<K, 2>(v);
+  return t32_partial<K, 1>(v);
+}
+
 // ---------------------------------------------------------------- device: per-head q/k RMSNorm + RoPE
 // The arithmetic of the fused q/k norm (qk_norm_rope_kv.hip) on the 8 + 8 elements one lane holds of a head row:
 // x1 = elements [e, e+8) of the first half, x2 = the same offsets of the second half (RoPE pairs x1[i], x2[i]).
 // Shared with the decode attention that applies it to its query rows, so both give the same bits.
 
-// This lane's part of the row's sum of squares (the row's lanes then sum their parts with group_sum).
-__device__ __forceinline__ float row_sumsq16(const float* x1, const float* x2) {
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    ss = __builtin_fmaf(x1[i], x1[i], ss);
-    ss = __builtin_fmaf(x2[i], x2[i], ss);
+// This lane's part of the sum of squares of one half, in torch's order for a row of D elements: D >= 128 -- ATen
+// threads of one 4-element vector each, the lane's two adjacent ones added (the first tree level); D = 64 -- one
+// element per thread, the tree's first three levels over the lane's 8 elements. The D/16 lanes of a row then add
+// these parts with group_sum<D/16> for each half, and the two halves' sums are the tree's last level.
+template <int D>
+__device__ __forceinline__ float half_sumsq8(const float* x) {
+  if constexpr (D >= 128) {
+    return sumsq4(x) + sumsq4(x + 4);
+  } else {
+    const float p0 = x[0] * x[0] + x[1] * x[1], p1 = x[2] * x[2] + x[3] * x[3];
+    const float p2 = x[4] * x[4] + x[5] * x[5], p3 = x[6] * x[6] + x[7] * x[7];
+    return (p0 + p1) + (p2 + p3);
   }
-  return ss;
 }
 
 // n = bf16(bf16(x * rstd) * w), then y1 = bf16(n1 cos - n2 sin), y2 = bf16(n2 cos + n1 sin), every product rounded
@@ -231,6 +316,13 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (LANES >= 32) v += __shfl_xor(v, 16, 64);
   if constexpr (LANES >= 64) v += __shfl_xor(v, 32, 64);
   return v;
+}
+
+// Sum of squares of a head row of D elements held as x1 / x2 (8 + 8 elements per lane, D/16 lanes, the fused
+// q/k norm's layout) in torch's order: each half's tree over its lanes, then the two halves added.
+template <int D>
+__device__ __forceinline__ float torch_row_sumsq(const float* x1, const float* x2) {
+  return group_sum<D / 16>(half_sumsq8<D>(x1)) + group_sum<D / 16>(half_sumsq8<D>(x2));
 }
 
 }  // namespace nvhip

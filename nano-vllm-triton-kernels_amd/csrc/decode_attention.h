@@ -137,20 +137,23 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
     const int64_t p = g.positions[b];
     const float* cs = g.cos_sin + (p < 0 ? 0 : p >= g.max_pos ? g.max_pos - 1 : p) * g.cs_st;
     // the query rows: lane group q8 / 8 = j0 holds the elements 8 j of the fused norm's lanes j = j0 + 4 u
-    // (chunk u of each half), so the sum of squares is rebuilt in that kernel's DPP order: lanes j ^ 1 and j ^ 2
-    // are lane groups 16 and 32 apart, and the last (mirror) step adds the two halves' partial sums
+    // (chunk u of each half), so the sum of squares is rebuilt in that kernel's (torch's) order: per half, lanes
+    // j ^ 1 and j ^ 2 are lane groups 16 and 32 apart and j ^ 4 is the other chunk u; then the two halves
     constexpr int HK = KC / 2;
-    float x1[HK][8], x2[HK][8], part[HK];
+    float x1[HK][8], x2[HK][8], p1[HK], p2[HK];
 #pragma unroll
     for (int u = 0; u < HK; ++u) {
       unpack8(__builtin_bit_cast(u32x4, qf[u]), x1[u]);
       unpack8(__builtin_bit_cast(u32x4, qf[u + HK]), x2[u]);
-      part[u] = row_sumsq16(x1[u], x2[u]);
-      part[u] += __shfl_xor(part[u], 16);
-      part[u] += __shfl_xor(part[u], 32);
+      p1[u] = half_sumsq8<D>(x1[u]);
+      p2[u] = half_sumsq8<D>(x2[u]);
+      p1[u] += __shfl_xor(p1[u], 16);
+      p2[u] += __shfl_xor(p2[u], 16);
+      p1[u] += __shfl_xor(p1[u], 32);
+      p2[u] += __shfl_xor(p2[u], 32);
     }
-    const float ss = HK == 1 ? part[0] : part[0] + part[HK - 1];
-    const float rstd = 1.0f / sqrtf(ss * g.inv_d + g.eps);
+    const float ss = HK == 1 ? p1[0] + p2[0] : (p1[0] + p1[HK - 1]) + (p2[0] + p2[HK - 1]);
+    const float rstd = torch_rsqrt(ss * g.inv_d + g.eps);
 #pragma unroll
     for (int u = 0; u < HK; ++u) {
       const int e = 32 * u + q8;
@@ -185,8 +188,7 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
         float k1[8], k2[8];
         unpack8(*reinterpret_cast<const u32x4*>(kr + e), k1);
         unpack8(*reinterpret_cast<const u32x4*>(kr + D / 2 + e), k2);
-        const float kss = group_sum<LN>(row_sumsq16(k1, k2));
-        const float krstd = 1.0f / sqrtf(kss * g.inv_d + g.eps);
+        const float krstd = torch_rsqrt(torch_row_sumsq<D>(k1, k2) * g.inv_d + g.eps);
         const u32x4 wa = *reinterpret_cast<const u32x4*>(g.k_w + e), wb = *reinterpret_cast<const u32x4*>(g.k_w + D / 2 + e);
         float c[8], s[8];
 #pragma unroll

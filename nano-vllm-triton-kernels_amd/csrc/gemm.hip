@@ -467,12 +467,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
 // ------------------------------------------------------------------------------------------------------------
 // RMSNorm (or Add+RMSNorm) of the A rows fused into the decode GEMM (M <= 32): the norm that precedes a projection
 // (input_layernorm -> qkv, post_attention_layernorm -> gate_up) in the same launch. Every block normalises the
-// 16 * MT rows it multiplies -- K = 64 * VPL * 8, 64 lanes per row, each lane the same VPL 16-byte vectors and the
-// same fp32 order as norm_kernel<64, VPL, ADD> (rms_norm.hip), so the normalised bf16 values are bitwise that
-// kernel's output -- into LDS, and the blocks of the first column tile also write the residual sum. The block's
-// W fragments (one round: K / 32 k steps over NW waves x U) are loaded before the norm, so the norm's loads and
-// reduction run under them; the A fragments then come from LDS. The per-column k order is that of gemm_skinny, so
-// the product is bitwise the two-launch result (norm, then matmul / matmul_silu_mul).
+// 16 * MT rows it multiplies -- K = 256 * KC, half a wave per row, each lane the same KC 16-byte chunks and the
+// same fp32 order as norm_kernel<32, KC, ADD> (rms_norm.hip, torch's order for M rows), so the normalised bf16
+// values are bitwise that kernel's output -- into LDS, and the blocks of the first column tile also write the
+// residual sum. The block's W fragments (one round: K / 32 k steps over NW waves x U) are loaded before the norm,
+// so the norm's loads and reduction run under them; the A fragments then come from LDS. The per-column k order is
+// that of gemm_skinny, so the product is bitwise the two-launch result (norm, then matmul / matmul_silu_mul).
 struct NormMfmaArgs {
   MfmaArgs g;              // g.a is not used: A = norm(x [+ r])
   const uint16_t* x;       // [M, K], row stride sx
@@ -480,13 +480,14 @@ struct NormMfmaArgs {
   const uint16_t* nw;      // norm weight [K]
   uint16_t* res_out;       // [M, K] contiguous: bf16(x + r) (ADD)
   int64_t sx, sr;
-  float inv_n, eps;
+  float factor, eps;       // the mean's factor for M rows (aten_mean_factor) and epsilon
+  int m;                   // aten_norm_bw(K, M) / 64
 };
 
-template <int MT, int NCOL, bool SILU, int VPL, bool ADD>
+template <int MT, int NCOL, bool SILU, int KC, bool ADD>
 __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
   constexpr int NW = 8;
-  constexpr int K = 64 * VPL * 8, KP = K + 8;  // LDS row pitch: the 16 rows of a fragment read hit distinct banks
+  constexpr int K = 256 * KC, KP = K + 8;  // LDS row pitch: the 16 rows of a fragment read hit distinct banks
   constexpr int U = K / 32 / NW;               // k steps per wave: the whole K in one round
   constexpr int R = 16 * MT;                   // rows of this block
   constexpr int NP = SILU ? 2 : 1;
@@ -514,60 +515,53 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
     }
   }
 
-  // the block's rows, normalised, into LDS (wave w: rows w, w + NW, ...; rows past M are zero). All of the wave's
-  // row loads are issued before the first store: the new-residual stores could alias the next rows' inputs for
-  // all the compiler knows, so loads written after them would have to wait for them.
-  constexpr int RW = R / NW;  // rows per wave
-  u32x4 raw[RW][VPL], rraw[RW][VPL], wraw[VPL];
+  // the block's rows, normalised, into LDS: half h = lane / 32 of wave w takes rows w + (2 i + h) NW, lane
+  // j = lane % 32 the chunks at elements 8 j + 256 k (rows past M are computed from row M - 1 and stored as zeros,
+  // so no lane leaves the reduction). All of the wave's row loads are issued before the first store: the
+  // new-residual stores could alias the next rows' inputs for all the compiler knows, so loads written after them
+  // would have to wait for them.
+  constexpr int RH = R / NW / 2;  // rows per half-wave
+  static_assert(RH * 2 * NW == R, "whole row pairs per wave");
+  const int half = lane / 32, cj = (lane % 32) * 8;
+  u32x4 raw[RH][KC], rraw[RH][KC], wraw[KC];
 #pragma unroll
-  for (int i = 0; i < RW; ++i) {
-    const int m = min(m0 + wave + i * NW, g.M - 1);
+  for (int i = 0; i < RH; ++i) {
+    const int m = min(m0 + wave + (2 * i + half) * NW, g.M - 1);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) raw[i][j] = load8<true>(a.x + int64_t(m) * a.sx + (j * 64 + lane) * 8);
+    for (int k = 0; k < KC; ++k) raw[i][k] = load8<true>(a.x + int64_t(m) * a.sx + 256 * k + cj);
     if constexpr (ADD)
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) rraw[i][j] = load8<true>(a.r + int64_t(m) * a.sr + (j * 64 + lane) * 8);
+      for (int k = 0; k < KC; ++k) rraw[i][k] = load8<true>(a.r + int64_t(m) * a.sr + 256 * k + cj);
   }
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) wraw[j] = load8<true>(a.nw + (j * 64 + lane) * 8);
+  for (int k = 0; k < KC; ++k) wraw[k] = load8<true>(a.nw + 256 * k + cj);
 #pragma unroll
-  for (int i = 0; i < RW; ++i) {
-    const int rl = wave + i * NW, m = m0 + rl;
+  for (int i = 0; i < RH; ++i) {
+    const int rl = wave + (2 * i + half) * NW, m = m0 + rl;
     uint16_t* dst = As + rl * KP;
-    if (m >= g.M) {
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) *reinterpret_cast<u32x4*>(dst + (j * 64 + lane) * 8) = u32x4{0, 0, 0, 0};
-      continue;
-    }
-    float v[VPL][8];
+    float v[KC][8];
     if constexpr (ADD) {
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) {
+      for (int k = 0; k < KC; ++k) {
         float xf[8], rf[8];
-        unpack8(raw[i][j], xf);
-        unpack8(rraw[i][j], rf);
+        unpack8(raw[i][k], xf);
+        unpack8(rraw[i][k], rf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[j][e] = xf[e] + rf[e];
-        if (blockIdx.x == 0) store8<true>(a.res_out + int64_t(m) * K + (j * 64 + lane) * 8, pack8(v[j]));
+        for (int e = 0; e < 8; ++e) v[k][e] = xf[e] + rf[e];
+        if (blockIdx.x == 0 && m < g.M) store8<true>(a.res_out + int64_t(m) * K + 256 * k + cj, pack8(v[k]));
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) unpack8(raw[i][j], v[j]);
+      for (int k = 0; k < KC; ++k) unpack8(raw[i][k], v[k]);
     }
-    float ss = 0.0f;
+    const float rstd = torch_rsqrt(group_sum<32>(t32_partial_m<KC>(v, a.m)) * a.factor + a.eps);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
-    ss = group_sum<64>(ss);
-    const float rstd = 1.0f / sqrtf(ss * a.inv_n + a.eps);
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
+    for (int k = 0; k < KC; ++k) {
       float wfl[8], o[8];
-      unpack8(wraw[j], wfl);
+      unpack8(wraw[k], wfl);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = round_bf16(v[j][e] * rstd) * wfl[e];
-      *reinterpret_cast<u32x4*>(dst + (j * 64 + lane) * 8) = pack8(o);
+      for (int e = 0; e < 8; ++e) o[e] = round_bf16(v[k][e] * rstd) * wfl[e];
+      *reinterpret_cast<u32x4*>(dst + 256 * k + cj) = m < g.M ? pack8(o) : u32x4{0, 0, 0, 0};
     }
   }
   __syncthreads();
@@ -841,23 +835,23 @@ int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   return launch_skinny_tile<1, 8, SILU>(g, s);
 }
 
-template <int MT, int NCOL, bool SILU, int VPL, bool ADD>
+template <int MT, int NCOL, bool SILU, int KC, bool ADD>
 int launch_skinny_norm_tile(const NormMfmaArgs& a, hipStream_t s) {
   const int nout = SILU ? a.g.N / 2 : a.g.N;
   const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((a.g.M + 16 * MT - 1) / (16 * MT))), block(512);
-  hipLaunchKernelGGL((gemm_skinny_norm<MT, NCOL, SILU, VPL, ADD>), grid, block, 0, s, a);
+  hipLaunchKernelGGL((gemm_skinny_norm<MT, NCOL, SILU, KC, ADD>), grid, block, 0, s, a);
   return check_launch("rms_norm_matmul");
 }
 
 // The block tiles of launch_skinny (without the 64-column one); K = 2048 keeps one 16-row tile per block so that
 // the normalised rows (16 x 2056 bf16) and the reduction buffer fit the LDS.
-template <bool SILU, int VPL, bool ADD>
+template <bool SILU, int KC, bool ADD>
 int launch_skinny_norm(const NormMfmaArgs& a, hipStream_t s) {
   const int64_t nout = SILU ? a.g.N / 2 : a.g.N, cols16 = (nout + 15) / 16;
-  if constexpr (VPL == 2)
-    if (a.g.M > 16 && cols16 >= 256) return launch_skinny_norm_tile<2, 16, SILU, VPL, ADD>(a, s);
-  if (cols16 * ((a.g.M + 15) / 16) >= 256) return launch_skinny_norm_tile<1, 16, SILU, VPL, ADD>(a, s);
-  return launch_skinny_norm_tile<1, 8, SILU, VPL, ADD>(a, s);
+  if constexpr (KC == 4)
+    if (a.g.M > 16 && cols16 >= 256) return launch_skinny_norm_tile<2, 16, SILU, KC, ADD>(a, s);
+  if (cols16 * ((a.g.M + 15) / 16) >= 256) return launch_skinny_norm_tile<1, 16, SILU, KC, ADD>(a, s);
+  return launch_skinny_norm_tile<1, 8, SILU, KC, ADD>(a, s);
 }
 
 template <bool SILU>
@@ -991,17 +985,18 @@ extern "C" int nvhip_rms_norm_matmul_bf16(void* out, void* residual_out, const v
   a.r = static_cast<const uint16_t*>(residual);
   a.nw = static_cast<const uint16_t*>(norm_w);
   a.res_out = static_cast<uint16_t*>(residual_out);
-  a.sx = sx, a.sr = sr, a.inv_n = 1.0f / float(K), a.eps = eps;
+  a.sx = sx, a.sr = sr, a.eps = eps;
+  a.factor = aten_mean_factor(K, M), a.m = aten_norm_bw(K, M) / 64;  // torch's order for a norm over M rows
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define NVHIP_NORM_MM(SI, V, AD) return launch_skinny_norm<SI, V, AD>(a, s)
   if (K == 1024) {
-    if (silu) { if (add) NVHIP_NORM_MM(true, 2, true); NVHIP_NORM_MM(true, 2, false); }
-    if (add) NVHIP_NORM_MM(false, 2, true);
-    NVHIP_NORM_MM(false, 2, false);
+    if (silu) { if (add) NVHIP_NORM_MM(true, 4, true); NVHIP_NORM_MM(true, 4, false); }
+    if (add) NVHIP_NORM_MM(false, 4, true);
+    NVHIP_NORM_MM(false, 4, false);
   }
-  if (silu) { if (add) NVHIP_NORM_MM(true, 4, true); NVHIP_NORM_MM(true, 4, false); }
-  if (add) NVHIP_NORM_MM(false, 4, true);
-  NVHIP_NORM_MM(false, 4, false);
+  if (silu) { if (add) NVHIP_NORM_MM(true, 8, true); NVHIP_NORM_MM(true, 8, false); }
+  if (add) NVHIP_NORM_MM(false, 8, true);
+  NVHIP_NORM_MM(false, 8, false);
 #undef NVHIP_NORM_MM
 }
 

@@ -9,16 +9,16 @@
 //                                  (if caches are given and 0 <= slot < num_slots; -1 = padding, skipped)
 //
 // Numerics are those of the torch code the kernel replaces (layers/layernorm.py:20-30 rms_forward,
-// layers/rotary_embedding.py:6-14 apply_rotary_emb), with its two bf16 roundings:
-//   rstd = 1 / sqrt(sum(x^2) / D + eps)            fp32, correctly rounded sqrt and divide
+// layers/rotary_embedding.py:6-14 apply_rotary_emb) as torch computes it eagerly on the GPU, bit for bit, with its
+// two bf16 roundings:
+//   rstd = rsqrt(sum(x^2) / D + eps)                fp32 sum in ATen's order, torch's rsqrt (common.h)
 //   n    = bf16(bf16(x * rstd) * w)                 RMSNorm output (bf16, as q_norm/k_norm return it)
 //   y1   = bf16(n1*cos - n2*sin), y2 = bf16(n2*cos + n1*sin)   n1/n2 the two halves, products rounded separately
 // The file is compiled with -ffp-contract=off so no product is fused into an add (torch rounds each product).
-// Only the fp32 sum of squares is added in a different order than torch's reduction.
 //
 // Mapping (wave64): a head row of D bf16 is handled by LANES = D/16 consecutive lanes; lane j of the group holds
 // elements [8j, 8j+8) of both halves (two 16-byte loads), so RoPE pairs x1[i] with x2[i] inside the lane and the
-// sum of squares is a LANES-wide DPP reduction. Row r of a token is q head r (r < Hq), k head r-Hq, or v head
+// sum of squares is a LANES-wide DPP reduction per half. Row r of a token is q head r (r < Hq), k head r-Hq, or v head
 // r-Hq-Hkv (R = Hq + 2*Hkv rows). One block per token (R*LANES threads): for Qwen3-0.6B (Hq 16, Hkv 8, D 128) a
 // block is 4 waves (q 0-7, q 8-15, k 0-7, v 0-7), each reading 2 KB and writing 2 KB. Each KV row write is one
 // contiguous 256-byte run at slot*Hkv*D + h*D. Very wide models (R*LANES > 1024) use a flattened row space.
@@ -111,13 +111,11 @@ __device__ __forceinline__ void process_row(const QkArgs& a, int64_t t, int r, i
     }
   }
 
-  // sum of squares (fp32; the order and the fused multiply-adds differ from torch's reduction, within the
-  // rounding of one bf16 step of the normalised value), then the norm and the rotation (common.h)
+  // sum of squares in torch's order, then the norm and the rotation (common.h)
   float x1[8], x2[8];
   unpack8(xa, x1);
   unpack8(xb, x2);
-  const float ss = group_sum<D / 16>(row_sumsq16(x1, x2));
-  const float rstd = 1.0f / sqrtf(ss * a.inv_d + a.eps);
+  const float rstd = torch_rsqrt(torch_row_sumsq<D>(x1, x2) * a.inv_d + a.eps);
   u32x4 oa, ob;
   norm_rope16(x1, x2, rstd, wa, wb, c, s, oa, ob);
 

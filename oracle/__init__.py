@@ -7,6 +7,11 @@ import it, and only as the checker or the timed CPU baseline; the product path (
 Functions and the reference code each one follows (paths in R3pere/nano-vllm-triton-kernels):
   rms_forward        nanovllm/layers/layernorm.py:20-30   (RMSNorm.rms_forward)
   add_rms_forward    nanovllm/layers/layernorm.py:32-44   (RMSNorm.add_rms_forward)
+  rms_forward_gpu, add_rms_forward_gpu
+                     the same two functions with the numerics torch gives them when they run eagerly on the GPU
+                     (the reference's torch path on an MI355X): the mean of squares in ATen's GPU summation order
+                     (aten_reduce, restated from torch's open-source ATen/native/hip/Reduce.cuh) and torch.rsqrt's
+                     double-precision evaluation rounded to float
   rope_cos_sin_cache nanovllm/layers/rotary_embedding.py:19-35 (RotaryEmbedding.__init__ cache)
   apply_rotary_emb   nanovllm/layers/rotary_embedding.py:6-14
   rotary_forward     nanovllm/layers/rotary_embedding.py:37-48 (RotaryEmbedding.forward)
@@ -27,8 +32,11 @@ How each is pinned (tests/test_oracle.py): closed forms in float64, hand-compute
 (identity rotation, norm preservation, relative-position dependence, scale invariance), and brute-force loops on
 tiny inputs. The reference ships no golden vectors for this path.
 """
+from oracle import aten_reduce  # noqa: F401
 from oracle.torch_ref import (  # noqa: F401
     add_rms_forward,
+    add_rms_forward_gpu,
+    rms_forward_gpu,
     apply_rotary_emb,
     matmul_fp64,
     paged_decode_attention,

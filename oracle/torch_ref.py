@@ -6,6 +6,8 @@ a bf16 rounding exactly where the reference's torch code has a `.to(bfloat16)` o
 """
 import torch
 
+from oracle import aten_reduce
+
 BF16 = torch.bfloat16
 
 
@@ -29,6 +31,31 @@ def add_rms_forward(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tenso
     mean_sq = s.pow(2).mean(dim=-1, keepdim=True)
     normed = s * torch.rsqrt(mean_sq + eps)
     return normed.to(x.dtype).mul_(weight), new_residual
+
+
+def _gpu_rstd(s: torch.Tensor, eps: float) -> torch.Tensor:
+    """rsqrt(mean(s^2) + eps) per row of the fp32 CPU tensor s [..., n] with torch's GPU numerics: the mean in
+    ATen's GPU summation order for that many rows (oracle.aten_reduce), the fp32 add of eps, and torch.rsqrt's
+    double-precision evaluation rounded to float."""
+    n = s.shape[-1]
+    rows = s.reshape(-1, n)
+    mean = torch.from_numpy(aten_reduce.mean_sq(rows.numpy(), rows.shape[0]))
+    var = mean + torch.tensor(eps, dtype=torch.float32)
+    return torch.rsqrt(var.double()).float().reshape(*s.shape[:-1], 1)
+
+
+def rms_forward_gpu(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """rms_forward (layers/layernorm.py:20-30) as torch computes it eagerly on an MI355X, restated on the CPU: the
+    same rounding points as rms_forward, with the GPU's mean and rsqrt (_gpu_rstd). x [..., n] bf16 on the CPU; the
+    rows of the call are all of x's rows (a [T, H, n] view is T * H rows)."""
+    xf = x.to(torch.float32)
+    return (xf * _gpu_rstd(xf, eps)).to(x.dtype).mul_(weight)
+
+
+def add_rms_forward_gpu(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """add_rms_forward (layers/layernorm.py:32-44) with torch's GPU numerics (see rms_forward_gpu)."""
+    s = x.to(torch.float32) + residual.to(torch.float32)
+    return (s * _gpu_rstd(s, eps)).to(x.dtype).mul_(weight), s.to(x.dtype)
 
 
 def rope_cos_sin_cache(head_size: int, max_position: int, base: float) -> torch.Tensor:
@@ -70,12 +97,14 @@ def store_kvcache(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cac
 
 
 def qk_norm_rope_kv(q, k, v, positions, q_weight, k_weight, eps, cos_sin_cache, k_cache, v_cache, slot_mapping,
-                    write_k):
+                    write_k, gpu_numerics=False):
     """The unfused pre-attention composition (models/qwen3.py:89-105 then layers/attention.py:64-76):
     q_norm and k_norm (rms_forward per head row), rotary_emb, then store_kvcache of the rotated k and raw v.
-    Mutates the caches (unless they are empty); returns (q_out [T, Hq, D] contiguous, k_out or None)."""
-    qn = rms_forward(q, q_weight, eps)
-    kn = rms_forward(k, k_weight, eps)
+    Mutates the caches (unless they are empty); returns (q_out [T, Hq, D] contiguous, k_out or None).
+    gpu_numerics: the norms as torch computes them on the GPU (rms_forward_gpu; CPU tensors only)."""
+    norm = rms_forward_gpu if gpu_numerics else rms_forward
+    qn = norm(q, q_weight, eps)
+    kn = norm(k, k_weight, eps)
     q_out, k_rot = rotary_forward(positions, qn, kn, cos_sin_cache)
     if k_cache.numel() > 0:
         store_kvcache(k_rot, v, k_cache, v_cache, slot_mapping)

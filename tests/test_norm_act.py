@@ -1,14 +1,19 @@
 """GPU parity of RMSNorm, Add+RMSNorm and SiLU x Mul (nvhip_rms_norm_bf16, nvhip_add_rms_norm_bf16,
-nvhip_silu_mul_bf16) against the CPU oracle.
+nvhip_silu_mul_bf16) against the oracle.
 
-Structure of the reference's tests/test_kernels_norm_act.py: every output within MAX_ULP = 2 bf16 ulps of the
-oracle (only the fp32 summation order of the mean of squares differs, which can move the normalised value across
-one bf16 rounding boundary, two after the weight multiply); the new residual of Add+RMSNorm has no reduction and
-must be bitwise equal. SiLU x Mul has no reduction either: it is bitwise equal to torch's own GPU silu (the oracle
-run on the GPU, which is what the reference's test compares against) and within 1 ulp of the CPU oracle, whose
-vectorised exp may differ from the device exp in the last fp32 bit.
-Cases: the reference's grid (rows 1/7/128/4097 x n 128/1024, strided q/k views, SiLU at 3072) plus the MI355X
-workload (T 1/32/2048/8192 at hidden 1024 and gate_up 2 x 3072) and shapes that take the fallback kernels.
+The reference's tests/test_kernels_norm_act.py allows MAX_ULP = 2 bf16 ulps against torch eager (its kernels sum
+the squares in their own order). These kernels are held to more: bitwise equality with the reference's torch code
+run eagerly on the same GPU (oracle.rms_forward / add_rms_forward on device tensors -- the "torch-eager backend"
+that end-to-end greedy decode must match token for token) and with oracle.rms_forward_gpu, the CPU restatement of
+those numerics (ATen's GPU summation order for the call's row count, torch.rsqrt's double evaluation). The only
+exception is a row width ATen splits over the waves of a block (n = 8192 with 8 or more rows), held to the
+reference's 2 ulps. Against the plain CPU oracle (torch's CPU reduction order) every output stays within 2 ulps.
+The new residual of Add+RMSNorm has no reduction and is bitwise everywhere. SiLU x Mul is bitwise equal to torch's
+GPU silu and within 1 ulp of the CPU oracle, whose vectorised exp may differ from the device exp in the last fp32
+bit.
+Cases: the reference's grid (rows 1/7/128/4097 x n 128/1024, strided q/k views, SiLU at 3072), the MI355X workload
+(T 1/32/2048/8192 at hidden 1024 and gate_up 2 x 3072), every row count 1..9 (ATen's order changes with it), and
+shapes that take the block-per-row kernel (other widths, unaligned rows).
 """
 import os
 
@@ -29,11 +34,28 @@ WORKLOAD_T = [1, 32, 2048, 8192]
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "norm_act_t16.npz")
 
 
+def torch_gpu_order(n, rows):
+    """Whether ATen reduces rows of n without splitting a row over waves (then the kernels are bitwise torch's)."""
+    try:
+        oracle.aten_reduce.reduce_config(n, rows)
+        return True
+    except NotImplementedError:
+        return False
+
+
 def check_rms(x, w):
     y = rms_norm(x.to(DEV), w.to(DEV), EPS)
     ref = oracle.rms_forward(x, w, EPS)
     assert y.shape == ref.shape and y.dtype == torch.bfloat16
     assert max_ulp(y, ref) <= MAX_ULP
+    n = x.shape[-1]
+    rows = x.numel() // n
+    torch_gpu = oracle.rms_forward(x.to(DEV), w.to(DEV), EPS)  # the reference's torch code, eager on this GPU
+    if torch_gpu_order(n, rows):
+        assert torch.equal(y, torch_gpu), "not bitwise torch-eager on the GPU"
+        assert torch.equal(y.cpu(), oracle.rms_forward_gpu(x, w, EPS))
+    else:
+        assert max_ulp(y, torch_gpu) <= MAX_ULP
 
 
 def check_add(x, r, w):
@@ -41,6 +63,13 @@ def check_add(x, r, w):
     y_ref, s_ref = oracle.add_rms_forward(x, r, w, EPS)
     assert max_ulp(y, y_ref) <= MAX_ULP
     assert torch.equal(s.cpu(), s_ref), "new residual must be bitwise"
+    n = x.shape[-1]
+    y_gpu, _ = oracle.add_rms_forward(x.to(DEV), r.to(DEV), w.to(DEV), EPS)
+    if torch_gpu_order(n, x.numel() // n):
+        assert torch.equal(y, y_gpu), "not bitwise torch-eager on the GPU"
+        assert torch.equal(y.cpu(), oracle.add_rms_forward_gpu(x, r, w, EPS)[0])
+    else:
+        assert max_ulp(y, y_gpu) <= MAX_ULP
     # in-place variant: same outputs, residual overwritten
     r_dev = r.to(DEV)
     y2, r2 = fused_add_rms_norm_(x.to(DEV), r_dev, w.to(DEV), EPS)
@@ -73,6 +102,40 @@ def test_qk_norm_strided_views(tokens):
         y = rms_norm(dev.view(-1, h, HEAD_DIM), w.to(DEV), EPS)
         ref = oracle.rms_forward(cpu.view(-1, h, HEAD_DIM), w, EPS)
         assert max_ulp(y, ref) <= MAX_ULP
+        assert torch.equal(y.view(-1, h, HEAD_DIM), oracle.rms_forward(dev.view(-1, h, HEAD_DIM), w.to(DEV), EPS))
+        assert torch.equal(y.cpu().view(-1, h, HEAD_DIM), oracle.rms_forward_gpu(cpu.view(-1, h, HEAD_DIM), w, EPS))
+
+
+@pytest.mark.parametrize("n", [64, 128, 256, 1024, 2048, 4096])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 6, 7, 8, 9, 16, 33])
+def test_every_row_count(rows, n):
+    # ATen's threads per row (and so its summation order) change with the row count below 8
+    g = torch.Generator("cpu").manual_seed(rows * 13 + n)
+    w = norm_weight(n, g)
+    x, r = bf16_randn((rows, n), g), bf16_randn((rows, n), g)
+    check_rms(x, w)
+    check_add(x, r, w)
+
+
+@pytest.mark.parametrize("n", [64, 100, 128, 256, 1024, 2048, 2560, 3072, 4096])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9, 32, 100, 2048])
+def test_aten_order_is_torch_gpu_mean(rows, n):
+    # pins oracle.aten_reduce: torch's own GPU mean of squares, bit for bit
+    g = torch.Generator("cpu").manual_seed(rows * 31 + n)
+    x = bf16_randn((rows, n), g).float()
+    got = x.to(DEV).pow(2).mean(dim=-1).cpu().numpy()
+    exp = oracle.aten_reduce.mean_sq(x.numpy())
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def test_rsqrt_is_torch_gpu_rsqrt():
+    # pins the double-precision rsqrt of oracle._gpu_rstd: torch.rsqrt on float tensors, every float in [0.25, 4)
+    # and a log-uniform sample over [1e-6, 1e6]
+    g = torch.Generator("cpu").manual_seed(5)
+    xs = torch.cat([torch.arange(0x3E800000, 0x40800000, dtype=torch.int64).to(torch.int32).view(torch.float32),
+                    torch.exp(torch.empty(1 << 20).uniform_(-14, 14, generator=g))])
+    got = torch.rsqrt(xs.to(DEV)).cpu()
+    assert torch.equal(got, torch.rsqrt(xs.double()).float())
 
 
 @pytest.mark.parametrize("n", [HEAD_DIM, HIDDEN])

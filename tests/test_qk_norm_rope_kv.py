@@ -2,8 +2,11 @@
 
 Structure of the reference's tests/test_kernels_qk_rope_kv.py, with the oracle (the reference's torch code restated,
 run on the CPU on the same seeded inputs) as the referee:
+  torch eager  q_out, k_out and both caches bitwise equal to the reference's torch composition (q_norm / k_norm,
+               rotary_emb, store_kvcache) run eagerly on the same GPU, and to oracle.qk_norm_rope_kv with
+               gpu_numerics (its CPU restatement: ATen's GPU summation order, torch.rsqrt's double evaluation).
   norm stage   the kernel with an identity rotation table (cos = 1, sin = 0, all positions 0) outputs exactly its
-               normed q and k: within MAX_ULP = 2 bf16 ulps of the oracle's rms_forward.
+               normed q and k: within MAX_ULP = 2 bf16 ulps of the CPU oracle's rms_forward (the reference's bar).
   rope stage   the kernel's real output equals, bitwise, the oracle's RoPE applied to the kernel's own normed q/k.
   KV write     written k rows equal k_out bitwise, v rows equal v bitwise, every unnamed row is untouched.
   end to end   q_out / k_out within the task's bf16 tolerance (rtol 1.6e-2, atol 1e-2) of the oracle.
@@ -115,6 +118,22 @@ def check_kv_write(case, k_out, cache):
         assert torch.equal(cache[i].view(-1, hkv, d)[untouched], case.cache0[i].view(-1, hkv, d)[untouched])
 
 
+def check_torch_eager(case, q_out, k_out, cache):
+    """Bitwise the reference's torch code run eagerly on the GPU, and its CPU restatement with GPU numerics."""
+    q, k, v = case.views(case.buf_dev)
+    cache_t = case.cache0.clone()
+    q_t, k_t = oracle.qk_norm_rope_kv(q, k, v, case.positions.clamp(max=MAX_POS - 1).to(DEV), case.q_w.to(DEV),
+                                      case.k_w.to(DEV), EPS, cos_sin_cache(case.d).to(DEV), cache_t[0], cache_t[1],
+                                      case.slots.to(DEV), True)
+    assert torch.equal(q_out, q_t) and torch.equal(k_out, k_t), "not bitwise torch-eager on the GPU"
+    assert torch.equal(cache, cache_t), "caches differ from torch-eager's store_kvcache"
+    qc, kc, vc = case.views(case.buf_cpu)
+    empty = torch.empty(0)
+    q_c, k_c = oracle.qk_norm_rope_kv(qc, kc, vc, case.positions.clamp(max=MAX_POS - 1), case.q_w, case.k_w, EPS,
+                                      cos_sin_cache(case.d), empty, empty, None, True, gpu_numerics=True)
+    assert torch.equal(q_out.cpu(), q_c) and torch.equal(k_out.cpu(), k_c)
+
+
 def check_case(case):
     # norm stage
     q_n, k_n, _ = case.run(identity_rope=True)
@@ -128,6 +147,7 @@ def check_case(case):
     assert torch.equal(k_out.cpu(), kr), "k rope stage not bitwise"
     # KV write
     check_kv_write(case, k_out, cache)
+    check_torch_eager(case, q_out, k_out, cache)
     # end to end
     q_e, k_e = case.oracle_end_to_end()
     check_end_to_end(q_out, q_e, q_n, q_ref)
