@@ -9,6 +9,9 @@ against the same committed numbers. bf16 tensors are stored as their uint16 bit 
                            slots. Outputs: q_out, k_out, the normed q/k (before RoPE) and the written
                            cache rows.
   norm_act_t16.npz         rms_norm / fused_add_rms_norm at hidden 1024 and 128, silu_and_mul at 2 x 3072, 16 rows.
+  The *_gpu arrays are the same outputs with the numerics torch gives the reference's code on the GPU
+  (oracle.rms_forward_gpu: ATen's GPU summation order, torch.rsqrt's double evaluation), which the kernels match
+  bit for bit.
   matmul_small.npz         fp32 and bf16 A @ B for (M, N, K) = (7, 33, 65) and (20, 40, 300); B stored [N, K].
 """
 import os
@@ -40,9 +43,13 @@ def make_qk(seed=0):
     k_cache = torch.zeros(64, 256, Hkv, D, dtype=torch.bfloat16)
     v_cache = torch.zeros_like(k_cache)
     q_out, k_out = oracle.qk_norm_rope_kv(q, k, v, positions, q_w, k_w, eps, cos_sin, k_cache, v_cache, slots, True)
+    empty = torch.empty(0)
+    q_gpu, k_gpu = oracle.qk_norm_rope_kv(q, k, v, positions, q_w, k_w, eps, cos_sin, empty, empty, None, True,
+                                          gpu_numerics=True)
     rows = slots.long()
     return dict(qkv=bits(qkv), q_weight=bits(q_w), k_weight=bits(k_w), positions=positions.numpy(),
                 slot_mapping=slots.numpy(), eps=np.float32(eps), q_out=bits(q_out), k_out=bits(k_out),
+                q_out_gpu=bits(q_gpu), k_out_gpu=bits(k_gpu),
                 q_normed=bits(oracle.rms_forward(q, q_w, eps)), k_normed=bits(oracle.rms_forward(k, k_w, eps)),
                 k_cache_rows=bits(k_cache.view(-1, Hkv, D)[rows]), v_cache_rows=bits(v_cache.view(-1, Hkv, D)[rows]))
 
@@ -57,7 +64,8 @@ def make_norm_act(seed=1):
         y_add, s = oracle.add_rms_forward(x, r, w, 1e-6)
         out.update({f"x_{n}": bits(x), f"r_{n}": bits(r), f"w_{n}": bits(w),
                     f"rms_{n}": bits(oracle.rms_forward(x, w, 1e-6)), f"add_y_{n}": bits(y_add),
-                    f"add_res_{n}": bits(s)})
+                    f"add_res_{n}": bits(s), f"rms_gpu_{n}": bits(oracle.rms_forward_gpu(x, w, 1e-6)),
+                    f"add_y_gpu_{n}": bits(oracle.add_rms_forward_gpu(x, r, w, 1e-6)[0])})
     gu = torch.randn(16, 6144, generator=g).to(torch.bfloat16)
     out.update(gate_up=bits(gu), silu=bits(oracle.silu_and_mul(gu)))
     return out

@@ -31,6 +31,10 @@ def test_qk_norm_rope_kv_fixture():
     q_out, k_out = oracle.qk_norm_rope_kv(q, k, v, positions, qw, kw, eps, oracle.rope_cos_sin_cache(D, 40960, 1e6),
                                           kc, vc, slots, True)
     assert torch.equal(q_out, u16(z, "q_out")) and torch.equal(k_out, u16(z, "k_out"))
+    empty = torch.empty(0)
+    q_g, k_g = oracle.qk_norm_rope_kv(q, k, v, positions, qw, kw, eps, oracle.rope_cos_sin_cache(D, 40960, 1e6),
+                                      empty, empty, None, True, gpu_numerics=True)
+    assert torch.equal(q_g, u16(z, "q_out_gpu")) and torch.equal(k_g, u16(z, "k_out_gpu"))
     assert torch.equal(oracle.rms_forward(q, qw, eps), u16(z, "q_normed"))
     assert torch.equal(oracle.rms_forward(k, kw, eps), u16(z, "k_normed"))
     rows = slots.long()
@@ -46,6 +50,8 @@ def test_norm_act_fixture():
         assert torch.equal(oracle.rms_forward(x, w, 1e-6), u16(z, f"rms_{n}"))
         y, s = oracle.add_rms_forward(x, r, w, 1e-6)
         assert torch.equal(y, u16(z, f"add_y_{n}")) and torch.equal(s, u16(z, f"add_res_{n}"))
+        assert torch.equal(oracle.rms_forward_gpu(x, w, 1e-6), u16(z, f"rms_gpu_{n}"))
+        assert torch.equal(oracle.add_rms_forward_gpu(x, r, w, 1e-6)[0], u16(z, f"add_y_gpu_{n}"))
     assert torch.equal(oracle.silu_and_mul(u16(z, "gate_up")), u16(z, "silu"))
 
 

@@ -166,9 +166,10 @@ def test_golden_t16():
     u16 = lambda name: torch.from_numpy(z[name].astype(np.int16)).view(torch.bfloat16)
     for n in (1024, 128):
         x, r, w = u16(f"x_{n}").to(DEV), u16(f"r_{n}").to(DEV), u16(f"w_{n}").to(DEV)
-        assert max_ulp(rms_norm(x, w, EPS), u16(f"rms_{n}")) <= MAX_ULP
+        y1 = rms_norm(x, w, EPS)
+        assert max_ulp(y1, u16(f"rms_{n}")) <= MAX_ULP and torch.equal(y1.cpu(), u16(f"rms_gpu_{n}"))
         y, s = fused_add_rms_norm(x, r, w, EPS)
-        assert max_ulp(y, u16(f"add_y_{n}")) <= MAX_ULP
+        assert max_ulp(y, u16(f"add_y_{n}")) <= MAX_ULP and torch.equal(y.cpu(), u16(f"add_y_gpu_{n}"))
         assert torch.equal(s.cpu(), u16(f"add_res_{n}"))
     assert max_ulp(silu_and_mul(u16("gate_up").to(DEV)), u16("silu")) <= 1
 

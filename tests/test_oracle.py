@@ -119,6 +119,80 @@ def test_rms_strided_3d_view_equals_rows():
                        oracle.rms_forward(q.reshape(80, 128).contiguous(), w, 1e-6))
 
 
+# ------------------------------------------------------------------ torch's GPU order (oracle.aten_reduce)
+# Bitwise against torch's own GPU mean in tests/test_norm_act.py (GPU); here: the launch shapes and hand-derived
+# known answers that a plausible slip in the restatement (sequential or pairwise order inside a thread, the wrong
+# threads per row for small row counts, the element loop of narrow rows) changes.
+
+@pytest.mark.parametrize("n,rows,expected", [
+    (64, 1, (False, 64)), (64, 2048, (False, 64)), (100, 8, (False, 64)), (128, 1, (True, 32)),
+    (128, 4096, (True, 32)), (1024, 1, (True, 256)), (1024, 3, (True, 256)), (1024, 4, (True, 128)),
+    (1024, 7, (True, 128)), (1024, 8, (True, 64)), (1024, 8192, (True, 64)), (2048, 1, (True, 512)),
+    (2048, 2, (True, 256)), (4096, 1, (True, 512)), (2560, 100, (True, 64))])
+def test_aten_launch_shapes(n, rows, expected):
+    assert oracle.aten_reduce.reduce_config(n, rows) == expected
+
+
+def test_aten_launch_shapes_not_restated():
+    for n, rows in ((8192, 8), (130, 8)):  # a row split over waves; misaligned vector loads
+        with pytest.raises(NotImplementedError):
+            oracle.aten_reduce.reduce_config(n, rows)
+
+
+def test_aten_order_known_answers():
+    big = np.float32(2 ** 24)  # 2^24 + 1 is a tie between 2^24 and 2^24 + 2 and rounds to 2^24 (even)
+    # n = 128 (32 threads, one 4-vector each): ((2^24 + 1) + 1) + 1 = 2^24; pairs would give 2^24 + 2
+    y = np.zeros((1, 128), np.float32)
+    y[0, :4] = [big, 1, 1, 1]
+    assert oracle.aten_reduce.row_sum(y)[0] == big
+    # n = 64 (64 threads of one element, then a tree of adjacent pairs): (2^24 + 1) + (1 + 1) = 2^24 + 2
+    y = np.zeros((1, 64), np.float32)
+    y[0, :4] = [big, 1, 1, 1]
+    assert oracle.aten_reduce.row_sum(y)[0] == big + 2
+    # n = 1024: y[0] = 2^24, y[1..3] = 2, y[256] = y[512] = y[768] = 1 (exact sum 2^24 + 9)
+    y = np.zeros((1, 1024), np.float32)
+    y[0, :4] = [big, 2, 2, 2]
+    y[0, [256, 512, 768]] = 1
+    # >= 8 rows, 64 threads: thread 0 sums component 0 over vectors 0, 64, 128, 192 first: 2^24 (three ties),
+    # then ((2^24 + 2) + 2) + 2
+    assert oracle.aten_reduce.row_sum(y, 8)[0] == big + 6
+    # 4..7 rows, 128 threads: thread 0 = vectors 0 and 128 -> 2^24 + 6, thread 64 = vectors 64 and 192 -> 2,
+    # halving step: 2^24 + 8
+    assert oracle.aten_reduce.row_sum(y, 4)[0] == big + 8
+    # 1..3 rows, 256 threads: thread 0 = 2^24 + 6, + thread 128 (1) = 2^24 + 7 -> tie -> 2^24 + 8, + (1 + 1)
+    assert oracle.aten_reduce.row_sum(y, 1)[0] == big + 10
+    # the mean factor for a power-of-two width is 1/n exactly, whatever the row count
+    assert oracle.aten_reduce.mean_factor(1024, 12345) == np.float32(1 / 1024)
+
+
+@pytest.mark.parametrize("n", [64, 100, 128, 1024, 2560, 4096])
+@pytest.mark.parametrize("rows", [1, 4, 8])
+def test_aten_order_sums_every_term_once(n, rows):
+    # every element counted once: within the fp32 error bound of a sum of n positive terms of the float64 sum
+    rng = np.random.default_rng(n + rows)
+    y = rng.random((rows, n)).astype(np.float32) + 0.5
+    s = oracle.aten_reduce.row_sum(y).astype(np.float64)
+    exact = y.astype(np.float64).sum(axis=1)
+    assert np.all(np.abs(s - exact) <= n * 2.0 ** -23 * exact)
+    y2 = y.copy()
+    y2[:, n // 2] += 1.0  # one term changed by 1 moves the sum by ~1
+    assert np.all(np.abs(oracle.aten_reduce.row_sum(y2) - s - 1.0) < 1e-2 * exact.max() / n + 1e-3 * exact.max())
+
+
+def test_gpu_numerics_norms_close_to_cpu_oracle():
+    g = torch.Generator().manual_seed(8)
+    for rows, n in ((3, 1024), (33, 1024), (40, 128)):
+        x = torch.randn(rows, n, generator=g).to(BF16)
+        r = torch.randn(rows, n, generator=g).to(BF16)
+        w = (1 + 0.1 * torch.randn(n, generator=g)).to(BF16)
+        assert int(ulps(oracle.rms_forward_gpu(x, w, 1e-6), oracle.rms_forward(x, w, 1e-6)).max()) <= 2
+        y, s = oracle.add_rms_forward_gpu(x, r, w, 1e-6)
+        y_c, s_c = oracle.add_rms_forward(x, r, w, 1e-6)
+        assert int(ulps(y, y_c).max()) <= 2 and torch.equal(s, s_c)
+        y0, _ = oracle.add_rms_forward_gpu(x, torch.zeros_like(x), w, 1e-6)
+        assert torch.equal(y0, oracle.rms_forward_gpu(x, w, 1e-6))
+
+
 # ------------------------------------------------------------------ Add + RMSNorm
 
 def test_add_rms_residual_and_unrounded_sum():

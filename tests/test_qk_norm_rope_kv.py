@@ -213,6 +213,7 @@ def test_golden_t16():
     q_n, k_n, _, _ = run(torch.zeros_like(positions), identity_table(D))
     assert max_ulp(q_n, u16("q_normed")) <= MAX_ULP and max_ulp(k_n, u16("k_normed")) <= MAX_ULP
     q_out, k_out, kc, vc = run(positions, cos_sin_cache())
+    assert torch.equal(q_out.cpu(), u16("q_out_gpu")) and torch.equal(k_out.cpu(), u16("k_out_gpu"))
     check_end_to_end(q_out, u16("q_out"), q_n, u16("q_normed"))
     check_end_to_end(k_out, u16("k_out"), k_n, u16("k_normed"))
     rows = slots.long()
