@@ -4,7 +4,8 @@
  * One entry point per kernel family of nano-vllm's nanovllm/kernels/ package. Every entry point
  *   - takes raw device pointers, int64 sizes/strides (in elements), scalars and a hipStream_t (passed as void*);
  *   - launches asynchronously on that stream and returns 0 on success, or a negative NVHIP_E* code;
- *   - never allocates, synchronises or touches global mutable device state, so it may be recorded into a HIP graph;
+ *   - never allocates, synchronises or touches global mutable device state, so it may be recorded into a HIP graph
+ *     (nvhip_paged_decode_attention_bf16_noalloc alone uses a device array of the library, see there);
  *   - on failure stores a message readable with nvhip_last_error() (thread-local, valid until the next call).
  * bf16 tensors are passed as void* holding IEEE bfloat16 values (torch.bfloat16).
  * Size 0 (T == 0, rows == 0, M*N == 0) is a valid no-op that launches nothing.
@@ -151,6 +152,25 @@ int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_ca
                                       int64_t q_stride_head, int64_t out_stride_token, int64_t out_stride_head,
                                       float scale, int causal, void* workspace, int64_t workspace_size,
                                       void* stream);
+
+/*
+ * nvhip_paged_decode_attention_bf16 without a workspace argument and without any allocation: the context-split
+ * records go to a device array of this library (9 MiB per GPU, held until the process ends; its address on the
+ * current device is looked up once per device with hipGetSymbolAddress). No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, split policy and results as nvhip_paged_decode_attention_bf16 given a workspace
+ * of nvhip_paged_decode_attention_workspace_size(...) bytes; a need beyond the array is refused (NVHIP_EINVAL; the
+ * split policy never asks for more). All calls on one GPU share the array: calls that overlap in time on one GPU
+ * (different streams without ordering) race on it. The records need no initialisation (every block writes its own
+ * before the merge kernel reads it).
+ */
+int nvhip_paged_decode_attention_bf16_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                              const int32_t* block_table, const int32_t* context_lens,
+                                              int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D,
+                                              int64_t block_size, int64_t num_blocks, int64_t max_blocks,
+                                              int64_t q_stride_token, int64_t q_stride_head,
+                                              int64_t out_stride_token, int64_t out_stride_head, float scale,
+                                              int causal, void* stream);
 
 /*
  * Variable-length (prefill) attention.

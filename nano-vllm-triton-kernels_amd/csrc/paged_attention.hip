@@ -39,6 +39,8 @@
 // Tokens past the context, blocks outside [0, num_blocks) and rows past a query's causal limit take no part (their
 // K/V are not read; p = 0).
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "decode_attention.h"
 
@@ -302,4 +304,69 @@ extern "C" int nvhip_qk_norm_rope_kv_decode_attention_bf16(
   if (rows <= 4) return launch_decode<128, 4, true>(g, num_seqs, s);
   if (rows <= 8) return launch_decode<128, 8, true>(g, num_seqs, s);
   return launch_decode<128, 16, true>(g, num_seqs, s);
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Allocation-free variant: the split records live in `scratch`, a file-scope device array (each GPU the library
+// runs on holds its own copy until the process ends). The policy above makes fewer than 512 (sequence, kv head,
+// split) blocks whenever it splits, each with at most 16 rows of (2 + D <= 258) fp32, so kScratchBytes (9 MiB)
+// covers every size it can choose; a larger need is refused. In host code `scratch` is only a stand-in for the
+// symbol: its device address on the current GPU comes from hipGetSymbolAddress, looked up once per device on the
+// first call made with that device current, and only that address reaches the kernels.
+namespace nvhip {
+namespace {
+constexpr int64_t kScratchBytes = int64_t(9) << 20;
+constexpr int kScratchDevices = 64;
+}  // namespace
+}  // namespace nvhip
+
+static __device__ __align__(256) float scratch[nvhip::kScratchBytes / sizeof(float)];
+
+namespace nvhip {
+namespace {
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices] = {};
+
+// This GPU's scratch address (the current device's), or an error code.
+int scratch_address(float** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return invalid("paged_decode_attention_noalloc: no usable current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return invalid(std::string("paged_decode_attention_noalloc: hipGetSymbolAddress failed: ") +
+                     hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_ptr[dev];
+  return NVHIP_OK;
+}
+}  // namespace
+}  // namespace nvhip
+
+extern "C" int nvhip_paged_decode_attention_bf16_noalloc(void* out, const void* q, const void* k_cache,
+                                                         const void* v_cache, const int32_t* block_table,
+                                                         const int32_t* context_lens, int64_t num_seqs,
+                                                         int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D,
+                                                         int64_t block_size, int64_t num_blocks, int64_t max_blocks,
+                                                         int64_t q_stride_token, int64_t q_stride_head,
+                                                         int64_t out_stride_token, int64_t out_stride_head,
+                                                         float scale, int causal, void* stream) {
+  using namespace nvhip;
+  clear_error();
+  const int64_t need = nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, Hkv, D, block_size,
+                                                                   max_blocks);
+  if (need > kScratchBytes)
+    return invalid("paged_decode_attention_noalloc: the split records need " + std::to_string(need) +
+                   " bytes, more than the " + std::to_string(kScratchBytes) + "-byte scratch");
+  float* ws = nullptr;
+  if (need > 0 && num_seqs > 0)
+    if (int rc = scratch_address(&ws)) return rc;
+  return nvhip_paged_decode_attention_bf16(out, q, k_cache, v_cache, block_table, context_lens, num_seqs, q_len, Hq,
+                                           Hkv, D, block_size, num_blocks, max_blocks, q_stride_token,
+                                           q_stride_head, out_stride_token, out_stride_head, scale, causal, ws, need,
+                                           stream);
 }

@@ -38,6 +38,8 @@ SIGNATURES = {
     "nvhip_paged_decode_attention_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _i64, _f, _i, _p, _i64, _p],
     "nvhip_paged_decode_attention_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i64],
+    "nvhip_paged_decode_attention_bf16_noalloc": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                  _i64, _i64, _i64, _i64, _i64, _f, _i, _p],
     "nvhip_store_kvcache": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p],
     "nvhip_matmul_silu_mul_bf16": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "nvhip_prefill_attention_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -1,0 +1,65 @@
+"""nvhip_paged_decode_attention_bf16_noalloc (GPU): the paged decode attention whose context-split records live in
+the library's own device scratch array instead of a caller workspace. Called through the C ABI, it must give
+bitwise the output of nvhip_paged_decode_attention_bf16 with a workspace of the size that entry point asks for (the
+same split policy, the same kernels), on two calls in a row -- the second with a smaller batch and shorter
+contexts, so stale records of the first call would show. (Its refusal of sizes beyond the scratch cannot be
+reached with valid arguments: the split policy never needs more than the 9 MiB the array holds.)"""
+import pytest
+import torch
+
+from nanovllm_hip import _lib
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+HQ, HKV, D, BS = 16, 8, 128, 256
+
+
+def noalloc_fn():
+    return _lib.lib().nvhip_paged_decode_attention_bf16_noalloc
+
+
+def make_case(seed, batch, max_ctx):
+    g = torch.Generator("cpu").manual_seed(seed)
+    lens = torch.randint(max_ctx // 2, max_ctx + 1, (batch,), generator=g)
+    max_blocks = (max_ctx + BS - 1) // BS
+    nb = batch * max_blocks
+    kc = torch.randn(nb, BS, HKV, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(nb, BS, HKV, D, generator=g).to(torch.bfloat16).to(DEV)
+    bt = torch.randperm(nb, generator=g).to(torch.int32).view(batch, max_blocks).to(DEV)
+    q = torch.randn(batch, HQ, D, generator=g).to(torch.bfloat16).to(DEV)
+    return q, kc, vc, bt, lens.to(torch.int32).to(DEV), max_blocks
+
+
+def call(fn, case, out, extra):
+    q, kc, vc, bt, lens, max_blocks = case
+    B = q.shape[0]
+    args = [out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), lens.data_ptr(), B, 1, HQ,
+            HKV, D, BS, kc.shape[0], max_blocks, HQ * D, D, HQ * D, D, D ** -0.5, 1]
+    return fn(*args, *extra, torch.cuda.current_stream().cuda_stream)
+
+
+def test_noalloc_equals_workspace_entry_point_twice():
+    lib = _lib.lib()
+    fn = noalloc_fn()
+    for seed, batch, max_ctx in ((1, 4, 4096), (2, 2, 1100)):
+        case = make_case(seed, batch, max_ctx)
+        need = lib.nvhip_paged_decode_attention_workspace_size(batch, 1, HQ, HKV, D, BS, case[5])
+        assert need > 0, "the case must split its contexts (the scratch is used)"
+        ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+        ref = torch.empty(batch, HQ, D, dtype=torch.bfloat16, device=DEV)
+        _lib.check(call(lib.nvhip_paged_decode_attention_bf16, case, ref, [ws.data_ptr(), need]), "workspace call")
+        out = torch.full((batch, HQ, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+        _lib.check(call(fn, case, out, []), "noalloc call")
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"batch {batch}: differs from the workspace entry point"
+
+
+def test_noalloc_rejects_bad_arguments_before_launching():
+    fn = noalloc_fn()
+    B, max_blocks = 4, 16  # would split: the arguments are checked before the scratch is used
+    args = [None, None, None, None, None, None, B, 1, HQ, HKV, D, BS, 1, max_blocks, HQ * D, D, HQ * D, D, 0.1, 1,
+            None]
+    assert fn(*args) == _lib.NVHIP_EINVAL and "null pointer" in _lib.lib().nvhip_last_error().decode()
+    args[10] = 96  # head_dim
+    assert fn(*args) == _lib.NVHIP_EINVAL and "head_dim" in _lib.lib().nvhip_last_error().decode()
