@@ -246,7 +246,10 @@ int64_t nvhip_matmul_add_rms_norm_workspace_size(int64_t M, int64_t N, int64_t K
  * Each attention block (sequence b, kv head h) normalises and rotates its q rows with the arithmetic of the fused
  * kernel (the same bits) and the block whose key range holds the new token (position context_lens[b] - 1) writes
  * the new key (normed, rotated) and value of head h into slot slot_mapping[b] (skipped outside [0, num_blocks *
- * block_size)) before it reads the cache; the output is bitwise that of the two calls.
+ * block_size)) before it reads the cache; the output is bitwise that of the two calls when slot_mapping[b] is
+ * the slot of sequence b's position context_lens[b] - 1 in its block table (as every decode step builds it). A slot
+ * outside that layout is still written, but ordered before the reads of the writing block only: another block that
+ * reads it in the same launch (another context split of the pair, another sequence) may see the old row.
  *   q [num_seqs, Hq, D], k, v [num_seqs, Hkv, D]: the raw rows of the qkv projection (token strides q_stride,
  *   k_stride, v_stride, multiples of 8; heads contiguous; 16-byte aligned). positions int64, slot_mapping int32
  *   [num_seqs]; q_weight, k_weight [D]; cos_sin [max_pos, cos_sin_stride] fp32 (cos | sin); caches, block_table,

@@ -4,6 +4,3 @@ nanovllm_hip.kernels mirrors nano-vllm's nanovllm/kernels package (same function
 and assertion behaviour): qk_norm_rope_kv, rms_norm, fused_add_rms_norm, silu_and_mul, matmul. They run through
 the `nvhip` torch custom ops (nanovllm_hip.ops) on the C-ABI library libnvhip.so (include/nvhip.h).
 """
-import os
-
-PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))

@@ -44,7 +44,7 @@ class Batch:
             self.tables.append(perm[used:used + nb])
             used += nb
         self.max_blocks = max(need)
-        padded = [t + [0] * (self.max_blocks - len(t)) for t in self.tables]
+        padded = [t + [-1] * (self.max_blocks - len(t)) for t in self.tables]  # -1 padding (model_runner.py:273)
         self.block_tables = torch.tensor(padded, dtype=torch.int32, device=device)
         self.device = device
 

@@ -67,7 +67,7 @@ def prepare_mixed(reqs, block_size, device):
     """(input_ids, positions, Context, logits_indices) on `device` for a mixed step (model_runner.py:489-496)."""
     b = mixed_batch(reqs, block_size)
     max_blocks = max(len(r.block_table) for r in reqs)
-    tables = torch.tensor([r.block_table + [0] * (max_blocks - len(r.block_table)) for r in reqs],
+    tables = torch.tensor([r.block_table + [-1] * (max_blocks - len(r.block_table)) for r in reqs],
                           dtype=torch.int32, device=device)
 
     def dev(x, dtype):

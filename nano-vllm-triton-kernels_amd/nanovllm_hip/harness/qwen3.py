@@ -15,9 +15,10 @@ the separate launches), and torch's F.linear in the torch backend; forward(..., 
 backend use F.linear, the separate norms and the separate silu_and_mul, so that token differences come only from
 the four kernels.
 Both backends share the embedding and the attention. The attention is chosen apart
-from the backend: "torch" = the fp32 code below (prefill and decode), "hip" = the HIP paged decode attention
-(nanovllm_hip.kernels.attention, the flash_attn_with_kvcache call of layers/attention.py:84-90) for decode steps,
-the fp32 code for prefill.
+from the backend: "torch" = the fp32 code below (prefill and decode), "hip" = the HIP attention kernels
+(nanovllm_hip.kernels.attention): flash_attn_varlen_func for prefill and mixed steps (layers/attention.py:77-83),
+flash_attn_with_kvcache for decode steps (:84-90) -- or, in the hip backend, the decode step's fused q/k norm + RoPE
++ KV write + attention launch.
 """
 from dataclasses import dataclass
 
@@ -55,7 +56,7 @@ class Context:
     is_prefill: bool
     slot_mapping: torch.Tensor          # [T] int32, -1 = no KV write
     context_lens: torch.Tensor | None = None   # decode: [B] int32
-    block_tables: torch.Tensor | None = None   # decode / varlen prefill: [B, max_blocks] int32 (padded with 0)
+    block_tables: torch.Tensor | None = None   # decode / varlen prefill: [B, max_blocks] int32 (padded with -1)
     cu_seqlens_q: torch.Tensor | None = None   # varlen prefill: [B + 1] int32
     cu_seqlens_k: torch.Tensor | None = None
     max_seqlen_q: int = 0
@@ -185,10 +186,20 @@ class Deferred:
 # ------------------------------------------------------------------ the model
 
 class Qwen3:
-    """Random-init Qwen3 weights (bf16) and the forward pass with backend dispatch. Tied embeddings."""
+    """Random-init Qwen3 weights (bf16) and the forward pass with backend dispatch. Tied embeddings.
 
-    def __init__(self, cfg: Qwen3Config, device, seed=0):
+    The kernel backend is latched when the model is built, as the reference's layers read nanovllm.kernels.backend
+    in __init__ (layers/layernorm.py:18, layers/activation.py:13, models/qwen3.py:73): from nanovllm_hip.kernels
+    .backend ("hip" -> this package's kernels, "compile" -> the layers' torch code, here "torch") unless
+    kernel_backend names one. forward() runs the latched backend; its `backend` argument overrides it per call
+    (the decode harness runs both backends on one set of weights)."""
+
+    def __init__(self, cfg: Qwen3Config, device, seed=0, kernel_backend=None):
         self.cfg = cfg
+        latched = hip.backend if kernel_backend is None else kernel_backend
+        if latched not in hip.BACKENDS + ("torch",):
+            raise ValueError(f"kernel backend {latched!r}: expected one of {hip.BACKENDS}")
+        self.kernel_backend = "torch" if latched == "compile" else latched
         g = torch.Generator(device="cpu").manual_seed(seed)
         std = cfg.init_std
         H, D, hq, hkv, I = cfg.hidden_size, cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads, \
@@ -336,9 +347,10 @@ class Qwen3:
             return hip.fused_add_rms_norm_(h, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]
         return add_rms_forward(h, residual, self.final_norm_w, self.cfg.rms_norm_eps)[0]
 
-    def forward(self, input_ids, positions, ctx: Context, backend: str, attention: str = "torch",
+    def forward(self, input_ids, positions, ctx: Context, backend: str | None = None, attention: str = "torch",
                 linear: str = "hip"):
-        """Returns the final hidden states [T, hidden] (after the last norm)."""
+        """Returns the final hidden states [T, hidden] (after the last norm). backend None: the latched one."""
+        backend = self.kernel_backend if backend is None else backend
         h, residual = F.embedding(input_ids, self.embed), None
         for li in range(len(self.layers)):
             q, k, v, residual = self.pre_attn(li, positions, h, residual, backend, linear)

@@ -1,7 +1,9 @@
 """The HIP kernels with the call signatures of nano-vllm's nanovllm/kernels package.
 
-`backend` plays the role of nanovllm/kernels/__init__.py:5: the layers read it once when they are built and
-dispatch on it ("hip" selects these kernels; "compile" keeps the layers' own torch code).
+`backend` plays the role of nanovllm/kernels/__init__.py:5 (set from Config.kernel_backend, model_runner.py:83):
+a model reads it once when it is built, as the reference's layers do in __init__ (layers/layernorm.py:18,
+layers/activation.py:13, models/qwen3.py:73), and dispatches on the value it latched ("hip" selects these kernels;
+"compile" keeps the layers' own torch code). The harness model nanovllm_hip.harness.qwen3.Qwen3 latches it so.
 """
 from nanovllm_hip.kernels.matmul import (add_rms_norm_matmul, matmul, matmul_add_rms_norm,  # noqa: F401
                                           matmul_silu_and_mul, rms_norm_matmul)

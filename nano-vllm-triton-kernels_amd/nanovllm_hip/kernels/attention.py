@@ -61,6 +61,10 @@ def qk_norm_rope_kv_decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.
     Hkv = k.shape[1]
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1)
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B
+    assert cache_seqlens.dtype == torch.int32 and cache_seqlens.shape == (B,)
+    assert k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.shape[3] == D
+    assert k_cache.dtype == v_cache.dtype == torch.bfloat16
     ok = (D in (64, 128) and Hq % Hkv == 0 and Hq // Hkv <= 16 and k.shape == v.shape == (B, Hkv, D)
           and all(t.dtype == torch.bfloat16 and t.stride(2) == 1 and t.stride(1) == D and t.stride(0) % 8 == 0
                   and t.data_ptr() % 16 == 0 for t in (q, k, v))

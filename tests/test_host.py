@@ -90,3 +90,25 @@ def test_no_cpu_fallback():
         matmul(x, x.t())
     with pytest.raises(NotImplementedError):
         qk_norm_rope_kv(**qk_args(device="cpu"))
+
+
+def test_model_latches_the_kernel_backend_at_construction():
+    # the reference's layers read nanovllm.kernels.backend once, in __init__ (layers/layernorm.py:18); so does the
+    # harness model, and a later change of the module value does not reach a model already built
+    import nanovllm_hip.kernels as kernels
+    from nanovllm_hip.harness.qwen3 import Qwen3, Qwen3Config
+    cfg = Qwen3Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                      num_attention_heads=2, num_key_value_heads=1, head_dim=64, max_position_embeddings=16)
+    old = kernels.backend
+    try:
+        kernels.backend = "compile"
+        model = Qwen3(cfg, "meta")
+        kernels.backend = "hip"
+        assert model.kernel_backend == "torch"
+        assert Qwen3(cfg, "meta").kernel_backend == "hip"
+        assert Qwen3(cfg, "meta", kernel_backend="compile").kernel_backend == "torch"
+        kernels.backend = "triton"
+        with pytest.raises(ValueError):
+            Qwen3(cfg, "meta")
+    finally:
+        kernels.backend = old
