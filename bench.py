@@ -7,11 +7,15 @@ Headline (`value`): the fused q/k RMSNorm + RoPE + paged-KV write at T = 8192 to
   bytes/launch = T * (4096 q read + 4096 q_out write + 8 position + 4 slot + 512 cos/sin)
                  + n_valid * (2048 k read + 2048 v read + 2048 k cache write + 2048 v cache write) + 512 weights
                = 16 908 * T + 512 with every slot valid (the reference's formula, scripts/bench_qk_rope_kv.py:50-52).
-One step = one launch over the T tokens. NSETS input/output sets (each with its own block table) rotate from
-launch to launch so that the working set (> 256 MB) does not stay in the Infinity Cache; the K timed launches are
-replayed from HIP graphs and timed with HIP events on the stream they run on.
+One step = one launch over the T tokens. NSETS = 8 input/output sets (each with its own block table) rotate from
+launch to launch, 544 MB of qkv in all (twice the 256 MiB Infinity Cache), so the reads come from HBM; exactly
+--steps launches are recorded into one HIP graph, warmed up by replaying it (--warmup launches and at least 50 ms),
+and one replay is timed with HIP events on the stream it runs on.
 
-Also reported (under "extra"): the same kernel at T = 1, 32, 2048; the unfused KV write (store_kvcache, bytes =
+Also reported (under "extra"): the ceilings of the headline on this part -- its own launch shape and memory pattern
+with the arithmetic removed (libnvhip_bench.so's nvhip_bench_qk_pattern) and a plain nontemporal copy of the same
+byte count; the same kernel at T = 1, 32, 2048, and at T = 2048 with write_k (the prefill setting of the
+reference's README table); the unfused KV write (store_kvcache, bytes =
 T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
@@ -20,8 +24,9 @@ prefill attention of one layer over 4 sequences of 2048 tokens and of a 256-toke
 TFLOP/s; the end-to-end decode step of a
 random-init Qwen3-0.6B-shaped model (batch 32, HIP graph: us per step, tokens/s, kernel nodes); a 256-token mixed
 step of the same model (16 decode requests + a 240-token prefill chunk), eager and from piecewise graphs.
-The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores) on a bounded
-sample of the same workload.
+The CPU baseline is the oracle (the reference's torch code restated, fp32 math, on the host cores this process may
+use, the count stated) on a bounded sample of the same workload, with CPU lines for RMSNorm, Add+RMSNorm, SiLU x Mul
+and the fp32 GEMM (torch.matmul) beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 8192] [--no-cpu] [--no-extra] [--no-e2e]
        (profiling modes: --profile, --profile-gemm, --profile-e2e, --profile-prefill, --profile-chunk,
@@ -44,8 +49,8 @@ FP32_PEAK_TFLOPS = 157.3
 HQ, HKV, D, MAX_POS, THETA, BLOCK, EPS = 16, 8, 128, 40960, 1e6, 256, 1e-6
 NUM_BLOCKS = 512
 PAD = 64
-NSETS = 4
-WARM_S = 0.05  # minimum warm-up wall time of every extra measurement (clock ramp)
+NSETS = 8  # rotating input sets: 8 x 68 MB of qkv for the headline, twice the 256 MiB Infinity Cache
+WARM_S = 0.05  # minimum warm-up wall time of every measurement (clock ramp)
 GEMM_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}  # (K, N)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qk_norm_rope_kv_t8192_traffic.json")
 
@@ -91,10 +96,40 @@ class FusedWorkload:
         self.v_cache = torch.zeros_like(self.k_cache)
         self.n_valid = T
 
-    def call(self, i, qk_norm_rope_kv):
+    def call(self, i, qk_norm_rope_kv, write_k=False):
         s = self.sets[i % NSETS]
         return qk_norm_rope_kv(s["q"], s["k"], s["v"], s["positions"], self.q_w, self.k_w, EPS, self.cos_sin,
-                               self.k_cache, self.v_cache, s["slots"], False)
+                               self.k_cache, self.v_cache, s["slots"], write_k)
+
+    def pattern(self, i, bench_lib, torch):
+        """The same launch through nvhip_bench_qk_pattern: the kernel's loads and stores without its arithmetic."""
+        s = self.sets[i % NSETS]
+        if "q_out" not in s:
+            s["q_out"] = torch.empty(self.T, HQ, D, dtype=torch.bfloat16, device=s["buf"].device)
+        rc = bench_lib.nvhip_bench_qk_pattern(
+            s["q_out"].data_ptr(), s["q"].data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(), s["q"].stride(0),
+            s["k"].stride(0), s["v"].stride(0), s["positions"].data_ptr(), s["slots"].data_ptr(),
+            self.cos_sin.data_ptr(), MAX_POS, self.k_cache.data_ptr(), self.v_cache.data_ptr(), NUM_BLOCKS * BLOCK,
+            self.T, HQ, HKV, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, rc
+
+
+def bench_lib():
+    """libnvhip_bench.so (measurement-only kernels, built with the library), loaded after torch."""
+    import ctypes
+    path = os.path.join(ROOT, "nano-vllm-triton-kernels_amd", "nanovllm_hip", "libnvhip_bench.so")
+    lib = ctypes.CDLL(path)
+    p, i64, i = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.nvhip_bench_stream_copy.argtypes = [p, p, i64, i, p]
+    lib.nvhip_bench_qk_pattern.argtypes = [p, p, p, p, i64, i64, i64, p, p, p, i64, p, p, i64, i64, i64, i64, p]
+    return lib
+
+
+def stream_copy(torch, lib, dst, src, nbytes):
+    """Plain nontemporal 16-byte copy of nbytes, 8 blocks of 256 threads per CU (grid-stride)."""
+    rc = lib.nvhip_bench_stream_copy(dst.data_ptr(), src.data_ptr(), nbytes, 2048,
+                                     torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
 
 
 def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
@@ -139,9 +174,71 @@ def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
     return start.elapsed_time(end) / (reps * n_calls), reps * n_calls
 
 
+def time_steps(torch, fn, steps, warmup, min_warm_s):
+    """Exactly `steps` calls of fn(i) recorded into one HIP graph; the graph is replayed for warm-up (ceil(warmup /
+    steps) replays, and at least min_warm_s of wall time), then one replay -- the `steps` calls and nothing else --
+    is timed with HIP events on the stream it runs on. Returns milliseconds per call."""
+    ms, done = time_graph(torch, fn, steps, steps, warmup, min_warm_s)
+    assert done == steps
+    return ms
+
+
+def host_cores():
+    """(threads to use, description): the CPUs this process may run on (its affinity set), capped by the cgroup CPU
+    quota when there is one, with os.cpu_count() stated beside them."""
+    n = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else n
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()
+            if q != "max":
+                quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    threads = min(usable, quota) if quota else usable
+    return threads, f"os.cpu_count()={n}, affinity {usable} CPUs, cgroup quota {quota or 'none'}"
+
+
+def cpu_median(fn, budget_s, min_calls=3):
+    fn()  # warm up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_calls:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_extra(torch, oracle, budget_s=3.0):
+    """The oracle's RMSNorm, Add+RMSNorm, SiLU x Mul at T = 8192 (hidden 1024, gate_up 2 x 3072) and the fp32 GEMM
+    (torch.matmul on the CPU) at the qkv shape at M = 2048 and at 4096^3, each the median of a ~3 s sample."""
+    g = torch.Generator("cpu").manual_seed(4)
+    T, H, I = 8192, 1024, 3072
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    r = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    gu = torch.randn(T, 2 * I, generator=g).to(torch.bfloat16)
+    out = {}
+    for name, fn, nbytes in (("rms_norm_T8192", lambda: oracle.rms_forward(x, w, EPS), (2 * T * H + H) * 2),
+                             ("fused_add_rms_norm_T8192", lambda: oracle.add_rms_forward(x, r, w, EPS),
+                              (4 * T * H + H) * 2),
+                             ("silu_and_mul_T8192", lambda: oracle.silu_and_mul(gu), 3 * T * I * 2)):
+        med, n = cpu_median(fn, budget_s)
+        out[name] = {"GB/s": round(nbytes / med / 1e9, 2), "ms": round(med * 1e3, 2), "calls": n}
+    for name, (M, N, K) in (("gemm_fp32_qkv_M2048", (2048, 4096, 1024)), ("gemm_fp32_4096", (4096, 4096, 4096))):
+        a = torch.randn(M, K, generator=g)
+        b = torch.randn(K, N, generator=g)
+        med, n = cpu_median(lambda: torch.matmul(a, b), budget_s, min_calls=2)
+        out[name] = {"TFLOP/s": round(2 * M * N * K / med / 1e12, 3), "ms": round(med * 1e3, 1), "calls": n}
+    return out
+
+
 def cpu_baseline(torch, oracle, T, budget_s=12.0):
     """The oracle (torch CPU, fp32 math) on the same fused workload, timed on the host cores."""
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads, cores_desc = host_cores()
     torch.set_num_threads(threads)
     g = torch.Generator("cpu").manual_seed(1)
     buf = torch.randn(T, (HQ + 2 * HKV) * D + PAD, generator=g).to(torch.bfloat16)
@@ -155,18 +252,33 @@ def cpu_baseline(torch, oracle, T, budget_s=12.0):
     kc = torch.zeros(NUM_BLOCKS, BLOCK, HKV, D, dtype=torch.bfloat16)
     vc = torch.zeros_like(kc)
     run = lambda: oracle.qk_norm_rope_kv(q, k, v, positions, qw, kw, EPS, cos_sin, kc, vc, slots, False)
-    run()  # warm up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, calls = cpu_median(run, budget_s, min_calls=5)
     return {"value": round(fused_bytes(T, T) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle qk_norm_rope_kv (torch CPU fp32) at T={T}, {len(times)} calls in ~{budget_s:.0f} s, "
-                      f"median {med * 1e3:.1f} ms/call, {torch.get_num_threads()} threads"}
+            "sample": f"oracle qk_norm_rope_kv (torch CPU fp32) at T={T}, {calls} calls in ~{budget_s:.0f} s, "
+                      f"median {med * 1e3:.1f} ms/call, {torch.get_num_threads()} threads ({cores_desc})",
+            "extra": cpu_extra(torch, oracle)}
+
+
+def ceilings(torch, kernels, wl, steps, head_gbs):
+    """Bandwidth ceilings for the headline, measured on this part: the headline's own launch shape and memory
+    pattern with the arithmetic removed (nvhip_bench_qk_pattern), and a plain nontemporal copy moving the same
+    number of bytes (half read, half written), both over rotating buffers like the headline."""
+    lib = bench_lib()
+    nbytes = fused_bytes(wl.T, wl.n_valid)
+    ms = time_steps(torch, lambda i: wl.pattern(i, lib, torch), max(40, steps), 20, WARM_S)
+    pat = nbytes / (ms * 1e-3) / 1e9
+    half = nbytes // 2 // 16 * 16
+    bufs = [(torch.empty(half, dtype=torch.uint8, device=wl.cos_sin.device),
+             torch.empty(half, dtype=torch.uint8, device=wl.cos_sin.device)) for _ in range(NSETS)]
+    ms_c = time_steps(torch, lambda i: stream_copy(torch, lib, bufs[i % NSETS][0], bufs[i % NSETS][1], half),
+                      max(40, steps), 20, WARM_S)
+    cp = 2 * half / (ms_c * 1e-3) / 1e9
+    del bufs
+    return {"qk_pattern_copy_T8192": {"us": round(ms * 1e3, 3), "GB/s": round(pat, 1),
+                                      "frac_hbm": round(pat / HBM_PEAK_GBS, 4),
+                                      "headline_frac_of_it": round(head_gbs / pat, 4)},
+            "stream_copy_same_bytes": {"us": round(ms_c * 1e3, 3), "GB/s": round(cp, 1),
+                                       "frac_hbm": round(cp / HBM_PEAK_GBS, 4), "bytes": 2 * half}}
 
 
 def extras(torch, oracle, kernels, dev, steps):
@@ -176,6 +288,12 @@ def extras(torch, oracle, kernels, dev, steps):
         ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, max(40, steps), 20, WARM_S)
         out[f"qk_norm_rope_kv_T{T}"] = {"us": round(ms * 1e3, 3),
                                         "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1)}
+        if T == 2048:  # prefill setting of the reference's README table: k_out written too
+            ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv, True), NSETS, max(40, steps),
+                               20, WARM_S)
+            nb = fused_bytes(T, T, write_k=True)
+            out["qk_norm_rope_kv_T2048_write_k"] = {"us": round(ms * 1e3, 3), "bytes": nb,
+                                                    "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)}
     wl = FusedWorkload(8192, dev, torch, oracle, seed=5)
     ms, _ = time_graph(torch, lambda i: kernels.store_kvcache(wl.sets[i % NSETS]["k"], wl.sets[i % NSETS]["v"],
                                                               wl.k_cache, wl.v_cache, wl.sets[i % NSETS]["slots"]),
@@ -392,36 +510,47 @@ def e2e_mixed_step(torch, dev, decodes=16, chunk=240, layers=28, min_len=512, ma
     return out
 
 
-def copy_ceiling(torch, dev, mib=1024, reps=20):
-    """Device copy (torch copy_) of `mib` MiB: the practical read+write bandwidth ceiling, in GB/s."""
-    n = mib * 2 ** 20 // 2
-    src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
-    dst = torch.empty_like(src)
-    for _ in range(20):
-        dst.copy_(src)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    end.record()
-    end.synchronize()
-    ms = start.elapsed_time(end) / reps
-    return round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)
-
-
-def profile_run(torch, kernels, wl, steps):
+def profile_run(torch, oracle, kernels, wl, steps):
+    """Eager launches for rocprofv3 counter runs (no graph): the headline kernel, then the other HBM-bound kernels
+    at their bench sizes (RMSNorm / Add+RMSNorm / SiLU x Mul / store_kvcache at T = 8192, the fused kernel at
+    T = 2048 with write_k), `steps` launches each, then 5 plain copies of 256 MiB (nvhip_bench_stream_copy: 256 MiB
+    read + 256 MiB written each) that calibrate the byte counters."""
     for i in range(steps):
         wl.call(i, kernels.qk_norm_rope_kv)
     torch.cuda.synchronize()
-    n = 256 * 2 ** 20 // 4
-    src = torch.ones(n, dtype=torch.float32, device=wl.k_cache.device)
+    dev = wl.k_cache.device
+    g = torch.Generator("cpu").manual_seed(2)
+    T, H, I = 8192, HQ * D // 2, 3 * HQ * D // 2
+    xs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+    gus = [torch.randn(T, 2 * I, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
+    for i in range(steps):
+        kernels.rms_norm(xs[i % 2], w, EPS)
+    for i in range(steps):
+        kernels.fused_add_rms_norm(xs[i % 2], xs[(i + 1) % 2], w, EPS)
+    for i in range(steps):
+        kernels.silu_and_mul(gus[i % 2])
+    for i in range(steps):
+        s = wl.sets[i % NSETS]
+        kernels.store_kvcache(s["k"], s["v"], wl.k_cache, wl.v_cache, s["slots"])
+    torch.cuda.synchronize()
+    del xs, gus
+    wl2 = FusedWorkload(2048, dev, torch, oracle, seed=2048)
+    for i in range(steps):
+        wl2.call(i, kernels.qk_norm_rope_kv, True)
+    torch.cuda.synchronize()
+    lib = bench_lib()
+    n = 256 * 2 ** 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
-        dst.copy_(src)
+        stream_copy(torch, lib, dst, src, n)
     torch.cuda.synchronize()
-    print(f"profile: {steps} x qk_norm_rope_kv (T={wl.T}, {fused_bytes(wl.T, wl.n_valid)} algorithmic bytes each), "
-          f"5 x copy of {n * 4} bytes", flush=True)
+    print(f"profile: {steps} x qk_norm_rope_kv (T={wl.T}, {fused_bytes(wl.T, wl.n_valid)} algorithmic bytes each); "
+          f"{steps} x rms_norm ({(2 * T * H + H) * 2} B), fused_add_rms_norm ({(4 * T * H + H) * 2} B), "
+          f"silu_and_mul ({3 * T * I * 2} B), store_kvcache ({T * (4 * HKV * D * 2 + 4)} B) at T={T}; {steps} x "
+          f"qk_norm_rope_kv T=2048 write_k ({fused_bytes(2048, 2048, True)} B); 5 x stream copy of {n} bytes",
+          flush=True)
 
 
 def profile_gemm(torch, kernels, dev, steps, M):
@@ -466,9 +595,10 @@ def main():
                         "mixed step (16 decodes + a 240-token chunk) --steps times eagerly and --steps times from "
                         "piecewise graphs, and print the mixed-step line")
     p.add_argument("--profile", action="store_true",
-                   help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), then "
-                        "5 copies of 256 MiB (torch copy_, 256 MiB read + 256 MiB written each) to calibrate the "
-                        "byte counters; prints the launch list instead of the JSON line")
+                   help="for rocprofv3 counter runs: --steps eager launches of the headline kernel (no graph), of "
+                        "RMSNorm / Add+RMSNorm / SiLU x Mul / store_kvcache at T=8192 and of the fused kernel at "
+                        "T=2048 with write_k, then 5 plain copies of 256 MiB (256 MiB read + 256 MiB written each) "
+                        "to calibrate the byte counters; prints the launch list instead of the JSON line")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: only one GPU is measured (the kernel path has no collective: under "
@@ -500,10 +630,11 @@ def main():
     T = args.tokens
     wl = FusedWorkload(T, dev, torch, oracle)
     if args.profile:
-        profile_run(torch, kernels, wl, args.steps)
+        profile_run(torch, oracle, kernels, wl, args.steps)
         return
-    # 40 launches per graph (the NSETS sets in turn): graph-to-graph boundaries add a few us, amortised here
-    ms, steps_done = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), 40, args.steps, args.warmup)
+    # exactly --steps launches (the NSETS sets in turn) recorded into one graph; one replay is timed
+    ms = time_steps(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), args.steps, args.warmup, WARM_S)
+    steps_done = args.steps
     nbytes = fused_bytes(T, wl.n_valid)
     gbs = nbytes / (ms * 1e-3) / 1e9
     traffic = None
@@ -516,13 +647,14 @@ def main():
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"qk_norm_rope_kv Qwen3-0.6B attention (Hq 16, Hkv 8, D 128), T={T}, qkv view of "
                                f"[T, 4096+{PAD}], 4 sequences, 512x256-slot paged KV, all slots valid, write_k=False",
-                   "tokens": T, "bytes_per_step": nbytes, "rotating_sets": NSETS},
+                   "tokens": T, "bytes_per_step": nbytes, "rotating_sets": NSETS,
+                   "rotating_read_bytes": NSETS * T * ((HQ + 2 * HKV) * D + PAD) * 2},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
     }
     if not args.no_extra:
-        result["extra"] = extras(torch, oracle, kernels, dev, args.steps)
-        result["extra"]["copy_ceiling_GB/s"] = copy_ceiling(torch, dev)
+        result["extra"] = ceilings(torch, kernels, wl, args.steps, gbs)
+        result["extra"].update(extras(torch, oracle, kernels, dev, args.steps))
         if not args.no_e2e:
             result["extra"]["e2e_decode_step"] = e2e_decode_step(torch, dev)
             result["extra"]["e2e_mixed_step"] = e2e_mixed_step(torch, dev)
