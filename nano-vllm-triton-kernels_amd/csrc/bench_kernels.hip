@@ -1,9 +1,9 @@
 // Measurement-only kernels for bench.py (libnvhip_bench.so; not part of the nvhip C ABI): the bandwidth ceilings
 // the HBM-bound kernels are compared against on the same part.
 //
-//  nvhip_bench_stream_copy   dst[i] = src[i] over n 16-byte vectors, grid-stride, nontemporal stores: the plain
-//                            read + write ceiling for a given byte count (and the known-size kernel that calibrates
-//                            rocprof's FETCH_SIZE / WRITE_SIZE counters).
+//  nvhip_bench_stream_copy   dst[i] = src[i] over n 16-byte vectors, grid-stride, nontemporal loads and stores:
+//                            the plain read + write ceiling for a given byte count (and the known-size kernel that
+//                            calibrates rocprof's FETCH_SIZE / WRITE_SIZE counters).
 //  nvhip_bench_qk_pattern    the memory traffic of nvhip_qk_norm_rope_kv_bf16 (Qwen3 layout, D = 128, write_k off)
 //                            with the arithmetic taken out: one 256-thread block per token, LANES = 8 lanes per head
 //                            row holding two 16-byte chunks (the halves of RoPE), q rows copied to q_out, k and v rows
@@ -21,7 +21,7 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(u32x4* __restrict__ ds
                                                           int64_t n) {
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-    __builtin_nontemporal_store(src[i], dst + i);
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 struct PatternArgs {
@@ -64,7 +64,9 @@ __global__ __launch_bounds__(256) void qk_pattern_kernel(const PatternArgs a) {
     src = a.v + t * a.v_stride + (r - a.Hq - a.Hkv) * D;
     dst = a.v_cache + slot * (int64_t(a.Hkv) * D) + (r - a.Hq - a.Hkv) * D;
   }
-  u32x4 x1 = *reinterpret_cast<const u32x4*>(src + e), x2 = *reinterpret_cast<const u32x4*>(src + HALF + e);
+  // read once, with the nontemporal hint, as the kernel reads its rows
+  u32x4 x1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + e));
+  u32x4 x2 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + HALF + e));
   if (r < a.Hq + a.Hkv) {  // q and k rows read their cos / sin values as the kernel does
     const float* cs = a.cos_sin + pos * D;
     const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs + e), c1 = *reinterpret_cast<const f32x4*>(cs + e + 4);

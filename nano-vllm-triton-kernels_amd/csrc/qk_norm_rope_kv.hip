@@ -81,16 +81,16 @@ __device__ __forceinline__ void process_row(const QkArgs& a, int64_t t, int r, i
 
   if (kind == 2) {  // v: raw copy of the head row into the cache
     if (slot < 0) return;
-    const u32x4 v1 = load8<ALIGNED>(src + e);
-    const u32x4 v2 = load8<ALIGNED>(src + HALF + e);
+    const u32x4 v1 = load8_once<ALIGNED>(src + e);
+    const u32x4 v2 = load8_once<ALIGNED>(src + HALF + e);
     store_out<ALIGNED>(a.v_cache + cache_off + e, v1);
     store_out<ALIGNED>(a.v_cache + cache_off + HALF + e, v2);
     return;
   }
   if (kind == 1 && slot < 0 && a.k_out == nullptr) return;  // a k row with nowhere to go
 
-  const u32x4 xa = load8<ALIGNED>(src + e);
-  const u32x4 xb = load8<ALIGNED>(src + HALF + e);
+  const u32x4 xa = load8_once<ALIGNED>(src + e);
+  const u32x4 xb = load8_once<ALIGNED>(src + HALF + e);
   const uint16_t* w = kind == 0 ? a.q_w : a.k_w;
   const u32x4 wa = load8<ALIGNED>(w + e);
   const u32x4 wb = load8<ALIGNED>(w + HALF + e);

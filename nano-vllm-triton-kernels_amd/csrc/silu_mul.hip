@@ -49,8 +49,8 @@ __global__ __launch_bounds__(kBlock) void silu_mul_kernel(const SiluArgs a) {
     col[k] = (idx - row[k] * a.per_row.d) * 8;
     if (idx < a.total) {
       const uint16_t* xr = a.x + int64_t(row[k]) * a.x_stride + col[k];
-      gate[k] = load8<true>(xr);
-      up[k] = load8<true>(xr + a.n);
+      gate[k] = load8_once<true>(xr);
+      up[k] = load8_once<true>(xr + a.n);
     }
   }
 #pragma unroll
