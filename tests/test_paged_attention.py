@@ -5,7 +5,8 @@ bf16 inputs). Tolerance: the bf16 output tolerance rtol 1.6e-2, atol 1e-2. Cases
 (32 sequences, 16 q heads, 8 kv heads, head_dim 128, 256-slot blocks, contexts of 512..2048 tokens); context lengths
 around the 32-token chunk and the block size, 0 (padding) and 1; block sizes that are not a multiple of 32; head_dim
 64 and 256; GQA ratios 1, 4, 8; several query tokens per sequence with and without the causal mask; NaN in the
-unused slots of a sequence's last block and in blocks no sequence owns; graph capture and replay.
+unused slots of a sequence's last block and in blocks no sequence owns; graph capture and replay; ragged batches of
+1 .. 512 sequences (empty contexts among them) with and without the context split, repeated bitwise.
 """
 import math
 
@@ -152,6 +153,38 @@ def _abi_call(q, kc, vc, lens, bt, scale, causal, workspace):
         ws.numel() * 4 if ws is not None else 0, _lib.stream_of(q))
     _lib.check(status, "paged_decode_attention")
     return out.view(q.shape), need
+
+
+@pytest.mark.parametrize("B,max_len,block_size,seed", [
+    (1, 100, 256, 1),      # 8 (sequence, kv head) pairs of at most 4 chunks
+    (3, 20000, 256, 2),    # 24 pairs of up to 625 chunks: many splits each
+    (20, 300, 16, 3),      # 160 pairs, 16-slot blocks
+    (64, 1200, 256, 4),    # 512 pairs: one block per pair even with a workspace
+    (512, 64, 32, 5),      # 4096 short pairs
+])
+def test_ragged_batches(B, max_len, block_size, seed):
+    """Ragged batches (context lengths 0 .. max_len, a tenth of them 0), with and without a workspace: the oracle's
+    values, zeros for empty contexts, and the same bits on a second call."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    lens = torch.randint(0, max_len + 1, (B,), generator=g)
+    lens[torch.rand(B, generator=g) < 0.1] = 0
+    lens = lens.tolist()
+    q, kc, vc, lt, bt = make_case(lens, block_size=block_size, seed=seed, nan_unused=False)
+    ref = oracle.paged_decode_attention(q, kc, vc, lt, bt, 0.1, True)
+    dev = [t.to(DEV) for t in (q, kc, vc, lt, bt)]
+    split, need = _abi_call(*dev, 0.1, True, workspace=True)
+    again, _ = _abi_call(*dev, 0.1, True, workspace=True)
+    single, _ = _abi_call(*dev, 0.1, True, workspace=False)
+    if B * 8 >= 256:
+        assert need == 0                   # enough (sequence, kv head) pairs for the CUs: no split
+    if B == 3:
+        assert need > 0                    # few pairs over long contexts: split
+    assert torch.equal(split, again)
+    for out in (split, single):
+        torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert torch.all(split[b] == 0) and torch.all(single[b] == 0)
 
 
 @pytest.mark.parametrize("lens", [[300, 2048, 1, 777, 256, 512, 0, 1500], [5000, 17, 4096]])
