@@ -329,6 +329,17 @@ def extras(torch, oracle, kernels, dev, steps):
                                            "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
                                            "torch_linear_us": round(ms_ref * 1e3, 2)}
         del a, wt, b
+    # B row-major ([K, N], N-contiguous: the layout of the reference's own matmul test) at 2048 x 4096 x 1024
+    M, N, K = 2048, 4096, 1024
+    a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    b = torch.randn(K, N, generator=g).to(torch.bfloat16).to(dev)
+    ms, _ = time_graph(torch, lambda i: kernels.matmul(a, b), 4, max(40, steps), 20, WARM_S)
+    ms_ref, _ = time_graph(torch, lambda i: torch.matmul(a, b), 4, max(40, steps), 20, WARM_S)
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    out["gemm_bf16_b_rowmajor_2048x4096x1024"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                                  "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
+                                                  "torch_matmul_us": round(ms_ref * 1e3, 2)}
+    del a, b
     # decode-sized GEMMs are weight-bandwidth bound: rotate over enough weight copies (>= 512 MiB) that every call
     # reads its weight from HBM, as a decode step over 28 layers does
     for layer, (K, N) in GEMM_SHAPES.items():

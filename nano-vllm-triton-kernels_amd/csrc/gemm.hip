@@ -6,8 +6,9 @@
 // (round to nearest even) before the products, which is what a tf32 tensor-core product sees.
 //
 // Kernels:
-//   gemm_mfma_nt   bf16, A and B both K-contiguous (sak == 1, sbk == 1; B = W.t() of a [N, K] weight):
-//                  32x32x16 bf16 MFMA, register + LDS staged pipeline, GROUP_M-swizzled, XCD-aware tile order.
+//   gemm_mfma_nt   bf16, A K-contiguous and B K-contiguous (sbk == 1; B = W.t() of a [N, K] weight) or, BNM,
+//                  N-contiguous (sbn == 1; a row-major [K, N] B): 32x32x16 bf16 MFMA, register + LDS staged
+//                  pipeline, GROUP_M-swizzled, XCD-aware tile order.
 //   gemm_skinny    bf16 with M <= 32, same layout: 16 columns per block, K split over 8 waves, 16x16x32 MFMA.
 //   gemm_mfma_f32  fp32, A K-contiguous, B K- or N-contiguous: 32x32x2 fp32 MFMA (exact products, fp32 sums).
 //   gemm_generic   any dtype/strides/precision: 64x64 tile, 4x4 outputs per thread, fp32 FMA.
@@ -137,7 +138,7 @@ constexpr int kBK = 64;
 struct MfmaArgs {
   uint16_t* c;
   const uint16_t* a;
-  const uint16_t* w;  // B^T: element (n, k) at w + n*swn + k
+  const uint16_t* w;  // B^T: element (n, k) at w + n*swn + k; BNM kernels: B, element (k, n) at w + k*swn + n
   int M, N, K;
   int64_t sam, swn, scm;
   int splits = 1;      // PARTIAL kernels: K ranges; block b computes range b % splits of tile b / splits
@@ -173,7 +174,14 @@ __device__ __forceinline__ void unroll_steps(F& step, int kt) {
 // PARTIAL (split-K, for launches with few tiles): the block's K range is z * K / splits .. (z + 1) * K / splits and
 // its fp32 tile goes unrounded to ws[z] (N a multiple of BN, K / splits a multiple of 64 * RS); the consumer sums
 // the splits in order.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU = false, bool PARTIAL = false>
+// BNM: B is N-contiguous ([K, N] rows of stride swn, N a multiple of 8; the layout of a plain row-major B). Its
+// k-tile is staged as it lies, [64 k][BN n] with a row pitch of BN + 32 elements (rows 4 apart land 64 bytes apart
+// in the 256-byte bank space), and the B^T fragment of a 16-wide k step (lane l: column l % 32, k = 8 (l / 32) ..
+// +8) comes from two transpose reads ds_read_b64_tr_b16: lanes 4j + q of a 16-lane group address row kb + j,
+// columns nb + 4q .. +4, and lane i receives column nb + i of rows kb .. kb + 3 (then kb + 4 .. kb + 7). The k order
+// of every output, and so the result, is that of the K-contiguous kernel.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU = false, bool PARTIAL = false,
+          bool BNM = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const MfmaArgs g) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
@@ -181,7 +189,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   constexpr int AC = BM * 8 / NT, BC = BN * 8 / NT, CH = AC + BC;  // 16-byte chunks per thread per k-tile
   static_assert(AC >= 1 && BC >= 1 && AC * NT == BM * 8 && BC * NT == BN * 8, "tile too small for the block");
   static_assert(RS >= 1 && RS <= 8, "register stages");
-  constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
+  static_assert(!(BNM && (SILU || PARTIAL)), "N-contiguous B: plain products only");
+  constexpr int BPITCH = BN + 32;                                      // BNM: row pitch of the staged B k-tile
+  constexpr int STAGE = BM * kBK + (BNM ? kBK * BPITCH : BN * kBK);  // bf16 elements per LDS stage
   constexpr int OUT_PITCH = BN + 8;
   constexpr int LDS_ELEMS = (2 * STAGE > BM * OUT_PITCH) ? 2 * STAGE : BM * OUT_PITCH;
   constexpr int NMF = FM * FN;            // MFMAs per 16-wide k step
@@ -202,13 +212,22 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // chunk i < AC: A chunk c = tid + NT*i; else B chunk c = tid + NT*(i-AC). Row c/8, logical k-chunk c%8, stored
-  // in LDS at chunk (c%8) ^ ((row >> 1) & 7) of the row.
+  // in LDS at chunk (c%8) ^ ((row >> 1) & 7) of the row. BNM: B chunk c is k row c / (BN/8) of the k-tile, columns
+  // 8 (c % (BN/8)) .. +8 (clamped into [0, N)), stored at the same place of the staged tile.
   const uint16_t* src[CH];
   int dst[CH], kofs[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const bool isA = i < AC;
     const int c = tid + NT * (isA ? i : i - AC), row = c / 8, kc = c % 8;
+    if (BNM && !isA) {
+      constexpr int CPRB = BN / 8;
+      const int kr = c / CPRB, col = min(n0 + (c % CPRB) * 8, g.N - 8);
+      src[i] = g.w + int64_t(kbeg + kr) * g.swn + col;
+      dst[i] = BM * kBK + kr * BPITCH + (c % CPRB) * 8;
+      kofs[i] = kr;
+      continue;
+    }
     int wrow = min(n0 + row, g.N - 1);
     if constexpr (SILU) {
       const int n2 = g.N / 2, half = BN / 2;
@@ -219,7 +238,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
     kofs[i] = kc * 8;
   }
   auto gload1 = [&](int i, int k0) -> u32x4 {
-    if (!KTAIL || k0 + kofs[i] < g.K) return *reinterpret_cast<const u32x4*>(src[i] + k0);
+    const int64_t step = (BNM && i >= AC) ? int64_t(k0) * g.swn : int64_t(k0);  // k0 rows of B, or k0 elements
+    if (!KTAIL || k0 + kofs[i] < g.K) return *reinterpret_cast<const u32x4*>(src[i] + step);
     return u32x4{0, 0, 0, 0};
   };
   u32x4 r[RS][CH];
@@ -243,14 +263,24 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_mfma_nt(const Mfm
   __syncthreads();
 
   bf16x8_t af[2][FM], bfr[2][FN];
+  // BNM transpose reads: lane 4j + q of 16-lane group G addresses row 8 (G / 2) + j of the k step (and + 4),
+  // columns 16 (G % 2) + 4 q of the fragment
+  const int tr_row = 8 * (lane / 32) + (lane % 16) / 4, tr_col = 16 * ((lane / 16) & 1) + 4 * (lane % 4);
   auto load_frags = [&](const uint16_t* st, int kk, int fs) {
     const int chunk = ((2 * kk + frag_half) ^ swz) * 8;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       af[fs][i] = *reinterpret_cast<const bf16x8_t*>(&st[(wm * WM + i * 32 + frag_row) * kBK + chunk]);
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      bfr[fs][j] = *reinterpret_cast<const bf16x8_t*>(&st[BM * kBK + (wn * WN + j * 32 + frag_row) * kBK + chunk]);
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (BNM) {
+        const uint16_t* p = st + BM * kBK + (16 * kk + tr_row) * BPITCH + wn * WN + j * 32 + tr_col;
+        const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * BPITCH);
+        bfr[fs][j] = __builtin_bit_cast(bf16x8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+      } else {
+        bfr[fs][j] = *reinterpret_cast<const bf16x8_t*>(&st[BM * kBK + (wn * WN + j * 32 + frag_row) * kBK + chunk]);
+      }
+    }
   };
   load_frags(smem, 0, 0);
 
@@ -756,11 +786,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_f32(const F3
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU, bool BNM = false>
 int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   const int64_t tiles = int64_t((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   if (tiles > INT32_MAX) return invalid("matmul: matrix too large");
-  hipLaunchKernelGGL((gemm_mfma_nt<BM, BN, WAVES_M, WAVES_N, RS, KTAIL, SILU>), dim3(unsigned(tiles)),
+  hipLaunchKernelGGL((gemm_mfma_nt<BM, BN, WAVES_M, WAVES_N, RS, KTAIL, SILU, false, BNM>), dim3(unsigned(tiles)),
                      dim3(WAVES_M * WAVES_N * 64), 0, s, g);
   return check_launch("matmul");
 }
@@ -774,14 +804,14 @@ int launch_mfma(const MfmaArgs& g, hipStream_t s) {
 // flight (RS = 4) instead of 2 (M = 256: down 22.6 -> 15.8 us, o_proj 15.4 -> 11.0, qkv 9.9 -> 7.4; deeper
 // staging measured no faster, and none of it helps once every CU has a large tile). The k order of every tile
 // shape is the same, so the result does not depend on the choice.
-template <int RS, bool KTAIL, bool SILU>
+template <int RS, bool KTAIL, bool SILU, bool BNM = false>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   constexpr int kCUs = 256;
   const int64_t tiles64 = int64_t((g.M + 63) / 64) * ((g.N + 63) / 64);
   if (g.M <= 64 || tiles64 <= kCUs) {
     if constexpr (!KTAIL)
-      if (((g.K / kBK) & 3) == 0) return launch_mfma<64, 64, 2, 2, 4, false, SILU>(g, s);
-    return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU>(g, s);
+      if (((g.K / kBK) & 3) == 0) return launch_mfma<64, 64, 2, 2, 4, false, SILU, BNM>(g, s);
+    return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU, BNM>(g, s);
   }
   struct Shape { int bm, bn; double eff; };
   constexpr Shape shapes[] = {{256, 256, 1.0}, {256, 192, 1.0}, {128, 256, 0.95}, {128, 128, 0.85}, {64, 128, 0.75}};
@@ -793,12 +823,21 @@ int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
     if (i == 0 || cost < best_cost) best = i, best_cost = cost;
   }
   switch (best) {
-    case 0: return launch_mfma<256, 256, 4, 2, 1, KTAIL, SILU>(g, s);
-    case 1: return launch_mfma<256, 192, 4, 2, RS, KTAIL, SILU>(g, s);
-    case 2: return launch_mfma<128, 256, 2, 4, RS, KTAIL, SILU>(g, s);  // 8 waves of 64x64: 3 % faster than 4 of 64x128
-    case 3: return launch_mfma<128, 128, 2, 4, RS, KTAIL, SILU>(g, s);
-    default: return launch_mfma<64, 128, 2, 2, RS, KTAIL, SILU>(g, s);
+    case 0: return launch_mfma<256, 256, 4, 2, 1, KTAIL, SILU, BNM>(g, s);
+    case 1: return launch_mfma<256, 192, 4, 2, RS, KTAIL, SILU, BNM>(g, s);
+    case 2: return launch_mfma<128, 256, 2, 4, RS, KTAIL, SILU, BNM>(g, s);  // 8 waves of 64x64: 3 % faster than 4 of 64x128
+    case 3: return launch_mfma<128, 128, 2, 4, RS, KTAIL, SILU, BNM>(g, s);
+    default: return launch_mfma<64, 128, 2, 2, RS, KTAIL, SILU, BNM>(g, s);
   }
+}
+
+// N-contiguous B: the tile kernel at every M (the skinny kernels read K-contiguous W rows straight into MFMA
+// operands).
+int launch_mfma_bnm(const MfmaArgs& g, hipStream_t s) {
+  const int nk = (g.K + kBK - 1) / kBK;
+  if (g.K % kBK != 0) return launch_mfma_shape<1, true, false, true>(g, s);
+  if (nk % 2 == 0) return launch_mfma_shape<2, false, false, true>(g, s);
+  return launch_mfma_shape<1, false, false, true>(g, s);
 }
 
 // 8 waves per block; 4 k steps of loads per wave in flight for wide outputs and 8-column blocks, 8 for 16-column
@@ -915,6 +954,15 @@ extern "C" int nvhip_matmul(void* c, const void* a, const void* b, int64_t M, in
       MfmaArgs m{static_cast<uint16_t*>(c), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
                  int(M), int(N), int(K), sam, sbn, scm};
       return launch_mfma_auto<false>(m, s);
+    }
+    // MFMA path for an N-contiguous B ([K, N] row-major): 16-byte aligned rows of A (K-contiguous) and B, N % 8 == 0
+    const bool nn = sak == 1 && sbn == 1 && scn == 1 && K % 8 == 0 && K > 0 && N % 8 == 0 && sam % 8 == 0 &&
+                    sbk % 8 == 0 && aligned16(a) && aligned16(b) &&
+                    M < (int64_t(1) << 31) && N < (int64_t(1) << 31) && K < (int64_t(1) << 31);
+    if (nn) {
+      MfmaArgs m{static_cast<uint16_t*>(c), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                 int(M), int(N), int(K), sam, sbk, scm};
+      return launch_mfma_bnm(m, s);
     }
     return launch_generic<uint16_t, false>(g, s);
   }

@@ -54,6 +54,24 @@ def test_matmul(M, N, K, dtype, prec, b_transposed):
     check(a, b, prec, TOL[(dtype, prec)])
 
 
+@pytest.mark.parametrize("M,N,K", [(33, 4096, 1024), (100, 1024, 3072), (256, 6144, 1024), (2048, 4096, 1024),
+                                   (2048, 1024, 2048), (300, 200, 136), (65, 1000, 1000), (64, 8, 8)])
+def test_n_contiguous_b_is_bitwise_the_k_contiguous_product(M, N, K):
+    """bf16 with B row-major ([K, N], N-contiguous: the reference test's layout) runs the MFMA tile kernel with B
+    staged as it lies and read through transpose reads; for M > 32 the K-contiguous layout of the same B runs the
+    same tile shape and k order, so the two products are bitwise equal (and within the bf16 tolerance of fp64).
+    Covers N not a multiple of the tile (column clamp), K not a multiple of 64 (zero tail) and a strided B."""
+    g = torch.Generator("cpu").manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    wide = torch.randn(K, N + 64, generator=g).to(torch.bfloat16).to(DEV)
+    for b in (wide[:, :N].contiguous(), wide[:, :N]):   # row stride N, then N + 64
+        c = matmul(a, b)
+        ref_nt = matmul(a, b.t().contiguous().t())      # the same B, K-contiguous
+        assert torch.equal(c, ref_nt)
+    torch.testing.assert_close(c.cpu().double(), oracle.matmul_fp64(a.cpu(), b.cpu()), rtol=1.6e-2,
+                               atol=1e-2 * math.sqrt(K))
+
+
 def test_ieee_is_not_tf32():
     g = torch.Generator("cpu").manual_seed(0)
     a = torch.randn(256, 4096, generator=g).to(DEV)
