@@ -6,8 +6,8 @@ With --linear torch both backends run the same projections (torch's F.linear) an
 of the path (RMSNorm, Add+RMSNorm, the fused q/k norm + RoPE + KV write, SiLU x Mul; with the HIP attention also the
 decode step's fused pre-attention + attention launch). Those are bitwise torch-eager on the GPU, so every generated
 token must be identical: the full-size case is the north star's batch-32 decode (28 layers, 32 requests with
-prompts of U[512, 2048] random ids, 8 decode steps). With --linear hip the projections run on the HIP GEMM, whose
-fp32 sums are in another order than hipBLASLt's: tokens may then differ where the torch backend's own top two logits
+prompts of U[512, 2048] random ids, 32 decode steps: 1056 tokens). With --linear hip the projections run on the HIP
+GEMM, whose fp32 sums are in another order than hipBLASLt's: tokens may then differ where the torch backend's own top two logits
 are within a bf16 step (nano-vllm's tests/test_greedy.py reports cross-backend agreement rather than requiring it
 for that reason); every such divergence must be such a near-tie. In every mode the graph replay gives exactly the
 eager tokens (the reference's MUST_MATCH pairs), and the hip decode step launches fewer kernels than the torch one.
@@ -49,17 +49,18 @@ def test_decode_small(attention, linear, fp32_logits):
 
 
 def test_decode_batch32_full_model_token_identical():
-    """The north star's batch-32 decode at full size: the four kernels only (--linear torch): 32 x 9 tokens."""
-    out = run(["--layers", "28", "--batch", "32", "--steps", "8", "--min-len", "512", "--max-len", "2048",
+    """The north star's batch-32 decode at full size: the four kernels only (--linear torch), 32 decode steps after
+    the first token: 32 x 33 tokens, every one identical to the torch-eager backend's."""
+    out = run(["--layers", "28", "--batch", "32", "--steps", "32", "--min-len", "512", "--max-len", "2048",
                "--reps", "2", "--linear", "torch"])
     agree = out["tokens_hip_vs_torch_eager"]
-    assert agree["total"] == 32 * 9
+    assert agree["total"] == 32 * 33
     assert agree["identical"] == agree["total"], out["divergence"]
 
 
 def test_decode_batch32_full_model_hip_gemm():
     """The same decode with the HIP GEMM for every projection and the LM head: graph = eager, and every request
     that diverges from torch-eager does so at a near-tie of the torch backend's logits."""
-    out = run(["--layers", "28", "--batch", "32", "--steps", "8", "--min-len", "512", "--max-len", "2048",
+    out = run(["--layers", "28", "--batch", "32", "--steps", "32", "--min-len", "512", "--max-len", "2048",
                "--reps", "2", "--linear", "hip"])
     check_near_ties(out)
