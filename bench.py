@@ -15,7 +15,7 @@ and one replay is timed with HIP events on the stream it runs on.
 Also reported (under "extra"): the ceilings of the headline on this part -- its own launch shape and memory pattern
 with the arithmetic removed (libnvhip_bench.so's nvhip_bench_qk_pattern) and a plain nontemporal copy of the same
 byte count; the same kernel at T = 1, 32, 2048, and at T = 2048 with write_k (the prefill setting of the
-reference's README table); the unfused KV write (store_kvcache, bytes =
+reference's README table; at T = 2048 enough sets rotate -- 32 -- that the reads come from HBM, as for the headline); the unfused KV write (store_kvcache, bytes =
 T * (2 * 2048 read + 2 * 2048 written + 4 slot)) at T = 8192; RMSNorm, Add+RMSNorm and SiLU x Mul at T = 8192
 (hidden 1024, gate_up 2 x 3072) in GB/s; the bf16 GEMM at the Qwen3-0.6B projection shapes, M = 2048 in TFLOP/s
 and M = 32 in GB/s (weights rotated through >= 512 MiB of copies so they come from HBM); the fp32 4096^3 GEMM;
@@ -50,6 +50,7 @@ HQ, HKV, D, MAX_POS, THETA, BLOCK, EPS = 16, 8, 128, 40960, 1e6, 256, 1e-6
 NUM_BLOCKS = 512
 PAD = 64
 NSETS = 8  # rotating input sets: 8 x 68 MB of qkv for the headline, twice the 256 MiB Infinity Cache
+MALL_BYTES = 256 * 2 ** 20  # the Infinity Cache (memory-attached last-level cache) of the part
 WARM_S = 0.05  # minimum warm-up wall time of every measurement (clock ramp)
 GEMM_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}  # (K, N)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qk_norm_rope_kv_t8192_traffic.json")
@@ -78,11 +79,12 @@ def block_table_slots(T, g, torch):
 
 
 class FusedWorkload:
-    def __init__(self, T, dev, torch, oracle, seed=0):
+    def __init__(self, T, dev, torch, oracle, seed=0, nsets=None):
         g = torch.Generator("cpu").manual_seed(seed)
         self.T = T
+        self.nsets = NSETS if nsets is None else nsets
         self.sets = []
-        for _ in range(NSETS):
+        for _ in range(self.nsets):
             buf = torch.randn(T, (HQ + 2 * HKV) * D + PAD, generator=g).to(torch.bfloat16).to(dev)
             q = buf[:, :HQ * D].view(T, HQ, D)
             k = buf[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D)
@@ -97,13 +99,13 @@ class FusedWorkload:
         self.n_valid = T
 
     def call(self, i, qk_norm_rope_kv, write_k=False):
-        s = self.sets[i % NSETS]
+        s = self.sets[i % self.nsets]
         return qk_norm_rope_kv(s["q"], s["k"], s["v"], s["positions"], self.q_w, self.k_w, EPS, self.cos_sin,
                                self.k_cache, self.v_cache, s["slots"], write_k)
 
     def pattern(self, i, bench_lib, torch):
         """The same launch through nvhip_bench_qk_pattern: the kernel's loads and stores without its arithmetic."""
-        s = self.sets[i % NSETS]
+        s = self.sets[i % self.nsets]
         if "q_out" not in s:
             s["q_out"] = torch.empty(self.T, HQ, D, dtype=torch.bfloat16, device=s["buf"].device)
         rc = bench_lib.nvhip_bench_qk_pattern(
@@ -284,12 +286,15 @@ def ceilings(torch, kernels, wl, steps, head_gbs):
 def extras(torch, oracle, kernels, dev, steps):
     out = {}
     for T in (1, 32, 2048):
-        wl = FusedWorkload(T, dev, torch, oracle, seed=T)
-        ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), NSETS, max(40, steps), 20, WARM_S)
+        # T = 2048: enough input sets (>= 2x the 256 MiB Infinity Cache, as for the headline) that every call reads
+        # from HBM; T = 1 / 32 are launch-latency bound and keep NSETS
+        nsets = NSETS if T <= 32 else max(NSETS, -(-(2 * MALL_BYTES) // (T * (HQ + 2 * HKV) * D * 2)))
+        wl = FusedWorkload(T, dev, torch, oracle, seed=T, nsets=nsets)
+        ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), nsets, max(40, steps), 20, WARM_S)
         out[f"qk_norm_rope_kv_T{T}"] = {"us": round(ms * 1e3, 3),
-                                        "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1)}
+                                        "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1), "sets": nsets}
         if T == 2048:  # prefill setting of the reference's README table: k_out written too
-            ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv, True), NSETS, max(40, steps),
+            ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv, True), nsets, max(40, steps),
                                20, WARM_S)
             nb = fused_bytes(T, T, write_k=True)
             out["qk_norm_rope_kv_T2048_write_k"] = {"us": round(ms * 1e3, 3), "bytes": nb,

@@ -125,8 +125,11 @@ __device__ __forceinline__ u32x4 load8(const uint16_t* p) {
   }
 }
 // load8 for data the kernel reads exactly once (activations streamed through): with ALIGNED a 16-byte load with
-// the nontemporal hint. Measured per kernel at T = 8192: the fused q/k norm kernel 26.4 -> 25.2 us and SiLU x Mul
-// 28.3 -> 26.5 us use it; RMSNorm (6.6 -> 7.5 us), Add+RMSNorm and store_kvcache were slower with it and do not.
+// the nontemporal hint. Measured per kernel at T = 8192 with the inputs in HBM: the fused q/k norm kernel 26.4 ->
+// 25.2 us and SiLU x Mul 28.3 -> 26.5 us use it; RMSNorm (6.6 -> 7.5 us), Add+RMSNorm and store_kvcache were slower
+// with it and do not. The hint's loads do not hit in the Infinity Cache: inputs still held there read slower with
+// it (the fused kernel at T = 2048 over 136 MB of rotating inputs: 7.3 us plain, 8.9 us nontemporal), and none of
+// the sc0 / sc1 / nt cache-policy combinations of a buffer load was faster in both cases.
 template <bool ALIGNED>
 __device__ __forceinline__ u32x4 load8_once(const uint16_t* p) {
   if constexpr (ALIGNED) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
