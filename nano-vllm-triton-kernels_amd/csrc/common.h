@@ -149,6 +149,29 @@ __device__ __forceinline__ void store8(uint16_t* p, const u32x4& v) {
   }
 }
 
+// 16-byte store (p 16-byte aligned) written through this XCD's L2 at device scope: a buffer store with the sc1
+// cache policy. The L2s of the 8 XCDs are not coherent with each other, so when a kernel ends its dirty L2 lines
+// are written back before the next kernel starts; with plain or nontemporal stores that write-back runs after the
+// last wave (bf16 GEMM at M = 2048, 16 MB of output: 3.0 us from the last block's end to the kernel's end, 0.3 us
+// with this store). Used where it measured faster: the fused q/k norm kernel and the MFMA GEMM epilogues. RMSNorm,
+// SiLU x Mul and the copy ceilings measured the same or slower, Add+RMSNorm 4 % and store_kvcache 13 % slower.
+// The buffer resource is based on the first active lane's address rounded down to 1 GiB; a lane whose address lies
+// in another 1 GiB window stores plainly.
+__device__ __forceinline__ void store16_wt(void* p, const u32x4& v) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a)) & 0xC0000000u;
+  const uint64_t b = (uint64_t(hi) << 32) | lo;
+  if ((a >> 30) == (b >> 30)) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(b), (short)0, 0x7fffffff, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(f32x4v, v), rs, uint32_t(a - b), 0, 16 /* sc1 */);
+  } else {
+    *reinterpret_cast<u32x4*>(p) = v;
+  }
+}
+
 // ---------------------------------------------------------------- RMSNorm in torch's GPU order
 // The reference's RMSNorm (layers/layernorm.py:20-44) run eagerly on the GPU computes mean(x^2) with ATen's generic
 // reduction and rsqrt with ATen's rsqrt kernel. The kernels here reproduce both bit for bit:
