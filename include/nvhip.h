@@ -264,6 +264,18 @@ int nvhip_qk_norm_rope_kv_decode_attention_bf16(
     int64_t block_size, int64_t num_blocks, int64_t max_blocks, int64_t out_stride_token, int64_t out_stride_head,
     float scale, void* workspace, int64_t workspace_size, void* stream);
 
+/*
+ * Greedy sampling: out[r] = the index of the largest of logits[r, 0 .. n) (int64), for bf16 logits with row
+ * stride row_stride (elements). Replaces the greedy branch of Sampler.forward (nanovllm/layers/sampler.py:9-10,
+ * logits.float().argmax(dim=-1)) and returns the same index: a NaN counts as the largest value, ties go to the
+ * smallest index. rows < 65536. workspace (16-byte aligned, contents need no initialisation) of
+ * nvhip_argmax_workspace_size(rows, n) bytes lets each row be split over several blocks and merged by a second
+ * launch; with a NULL (or too small) workspace one block reads each row.
+ */
+int64_t nvhip_argmax_workspace_size(int64_t rows, int64_t n);
+int nvhip_argmax_bf16(int64_t* out, const void* logits, int64_t rows, int64_t n, int64_t row_stride,
+                      void* workspace, int64_t workspace_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

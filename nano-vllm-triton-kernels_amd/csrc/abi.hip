@@ -28,6 +28,6 @@ int check_launch(const char* kernel) {
 
 }  // namespace nvhip
 
-extern "C" int nvhip_abi_version(void) { return 6; }
+extern "C" int nvhip_abi_version(void) { return 7; }
 
 extern "C" const char* nvhip_last_error(void) { return nvhip::g_last_error.c_str(); }

@@ -10,7 +10,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnvhip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 NVHIP_OK = 0
 NVHIP_EINVAL = -1
@@ -51,10 +51,12 @@ SIGNATURES = {
     "nvhip_qk_norm_rope_kv_decode_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64,
                                                     _f, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                                     _i64, _i64, _f, _p, _i64, _p],
+    "nvhip_argmax_workspace_size": [_i64, _i64],
+    "nvhip_argmax_bf16": [_p, _p, _i64, _i64, _i64, _p, _i64, _p],
 }
 RESTYPES = {"nvhip_last_error": ctypes.c_char_p, "nvhip_paged_decode_attention_workspace_size": ctypes.c_int64,
             "nvhip_prefill_attention_workspace_size": ctypes.c_int64,
-            "nvhip_matmul_add_rms_norm_workspace_size": ctypes.c_int64}
+            "nvhip_matmul_add_rms_norm_workspace_size": ctypes.c_int64, "nvhip_argmax_workspace_size": ctypes.c_int64}
 
 _lib = None
 

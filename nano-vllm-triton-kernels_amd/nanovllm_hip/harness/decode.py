@@ -2,8 +2,9 @@
 
 Like nano-vllm's scripts/bench_decode.py: B requests with random prompts are prefilled (one sequence at a time,
 eagerly), then every request gets one token per decode step. The decode step (model forward for the B last tokens,
-tied LM head, argmax) runs eagerly and as a recorded HIP graph whose static inputs are refreshed before each replay
-(model_runner.py:372-392, :647-698). Paged KV with 256-slot blocks; each request owns ceil((len + steps + 1) / 256)
+tied LM head, greedy argmax -- in the hip backend the HIP argmax over the bf16 logits, in the torch backend
+logits.float().argmax(-1), sampler.py:9-10) runs eagerly and as a recorded HIP graph whose static inputs are
+refreshed before each replay (model_runner.py:372-392, :647-698). Paged KV with 256-slot blocks; each request owns ceil((len + steps + 1) / 256)
 distinct random blocks.
 
 Reported: the generated tokens of each backend and mode, token agreement (hip vs torch eager, hip graph vs hip
@@ -27,6 +28,7 @@ import time
 import torch
 
 from nanovllm_hip.harness.qwen3 import Context, Qwen3, Qwen3Config
+from nanovllm_hip.kernels.sampler import greedy_sample
 
 BLOCK = 256
 
@@ -97,6 +99,10 @@ class DecodeStep:
     def forward(self):
         ctx = Context(False, self.slot_mapping, self.context_lens, self.batch.block_tables)
         h = self.model.forward(self.input_ids, self.positions, ctx, self.backend, self.attention, self.linear)
+        if self.backend == "hip" and not self.fp32_logits:
+            # greedy sampling on the bf16 logits (csrc/sampler.hip): the index of logits.float().argmax(-1)
+            logits = self.model.logits(h, False, self.backend, self.linear, as_float=False)
+            return logits, greedy_sample(logits)
         logits = self.model.logits(h, self.fp32_logits, self.backend, self.linear)
         return logits, logits.argmax(dim=-1)
 
@@ -137,7 +143,7 @@ def decode(model, batch, first, steps, backend, use_graph, reference=None, fp32_
         if reference is not None:
             for b in range(B):
                 if b not in diverged and reference[b][s] != nxt[b]:
-                    gap = float(logits[b, nxt[b]] - logits[b, reference[b][s]])
+                    gap = float(logits[b, nxt[b]].float() - logits[b, reference[b][s]].float())
                     diverged[b] = {"step": s, "logit_gap": round(gap, 5)}
         tokens.append(nxt)
         cur = nxt

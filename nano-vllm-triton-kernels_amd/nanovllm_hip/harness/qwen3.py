@@ -358,15 +358,14 @@ class Qwen3:
             h, residual = self.post_attn(li, o, residual, backend, linear)
         return self.final_norm(h, residual, backend)
 
-    def logits(self, h, fp32=False, backend="torch", linear="hip"):
-        """Tied LM head (embed_head.py:56-68): bf16 like the reference (then fp32 for sampling), or with fp32=True
-        the same product in fp32, which removes the exact ties of bf16-rounded logits. The hip backend's bf16 head
-        is the HIP GEMM (unless linear="torch")."""
+    def logits(self, h, fp32=False, backend="torch", linear="hip", as_float=True):
+        """Tied LM head (embed_head.py:56-68): bf16 like the reference (then fp32 for sampling, sampler.py:9; with
+        as_float=False the bf16 logits themselves), or with fp32=True the same product in fp32, which removes the
+        exact ties of bf16-rounded logits. The hip backend's bf16 head is the HIP GEMM (unless linear="torch")."""
         if fp32:
             return F.linear(h.float(), self.embed.float())
-        if backend == "hip" and linear == "hip":
-            return hip_linear(h, self.embed).float()
-        return F.linear(h, self.embed).float()
+        out = hip_linear(h, self.embed) if backend == "hip" and linear == "hip" else F.linear(h, self.embed)
+        return out.float() if as_float else out
 
 
 def num_params(cfg: Qwen3Config) -> int:

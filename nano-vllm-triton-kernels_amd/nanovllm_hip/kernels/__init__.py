@@ -9,6 +9,7 @@ from nanovllm_hip.kernels.matmul import (add_rms_norm_matmul, matmul, matmul_add
                                           matmul_silu_and_mul, rms_norm_matmul)
 from nanovllm_hip.kernels.qk_norm_rope_kv import qk_norm_rope_kv  # noqa: F401
 from nanovllm_hip.kernels.rms_norm import fused_add_rms_norm, fused_add_rms_norm_, rms_norm  # noqa: F401
+from nanovllm_hip.kernels.sampler import greedy_sample  # noqa: F401
 from nanovllm_hip.kernels.store_kvcache import store_kvcache  # noqa: F401
 from nanovllm_hip.kernels.swiglu import silu_and_mul  # noqa: F401
 

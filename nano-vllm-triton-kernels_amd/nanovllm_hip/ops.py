@@ -38,6 +38,7 @@ _DEF.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(
             "Tensor slot_mapping) -> ()")
 _DEF.define("paged_decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
             "Tensor context_lens, int q_len, float scale, bool causal) -> Tensor")
+_DEF.define("argmax(Tensor logits) -> Tensor")
 
 
 # ------------------------------------------------------------------ qk_norm_rope_kv
@@ -363,3 +364,24 @@ _DEF.impl("prefill_attention_out", _prefill_attention_out_impl, "CUDA")
 def _prefill_attention_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal,
                             block_table):
     return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+
+
+# ------------------------------------------------------------------ greedy sampling (argmax over the vocabulary)
+
+def _argmax_impl(logits):
+    rows, n = logits.shape
+    out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    ws_bytes = _lib.lib().nvhip_argmax_workspace_size(rows, n)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=logits.device)
+    status = _lib.lib().nvhip_argmax_bf16(out.data_ptr(), logits.data_ptr(), rows, n, logits.stride(0),
+                                          ws.data_ptr(), ws_bytes, _lib.stream_of(logits))
+    _lib.check(status, "argmax")
+    return out
+
+
+_DEF.impl("argmax", _argmax_impl, "CUDA")
+
+
+@torch.library.register_fake("nvhip::argmax")
+def _argmax_fake(logits):
+    return torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)

@@ -169,3 +169,17 @@ def test_rms_norm_matmul_rejects_bad_arguments_without_launching():
     assert call(x=ctypes.c_void_p((3 << 20) + 8)) == _lib.NVHIP_EINVAL and "aligned" in _err()
     assert call(res_out=ctypes.c_void_p((1 << 20) + 2048 * 16)) == _lib.NVHIP_EINVAL and "overlap" in _err()
     assert call(M=0) == _lib.NVHIP_OK and _err() == ""
+
+
+def test_argmax_rejects_bad_arguments_without_launching():
+    f = _lib.lib().nvhip_argmax_bf16
+    P = None
+    assert f(P, P, -1, 10, 10, P, 0, P) == _lib.NVHIP_EINVAL
+    assert f(P, P, 4, 0, 10, P, 0, P) == _lib.NVHIP_EINVAL
+    assert f(P, P, 4, 10, 9, P, 0, P) == _lib.NVHIP_EINVAL and "stride" in _err()
+    assert f(P, P, 65536, 10, 10, P, 0, P) == _lib.NVHIP_EINVAL and "rows" in _err()
+    assert f(P, P, 4, 10, 10, P, 0, P) == _lib.NVHIP_EINVAL and "null" in _err()
+    assert f(P, P, 0, 10, 10, P, 0, P) == _lib.NVHIP_OK and _err() == ""  # no rows: nothing launched
+    ws = _lib.lib().nvhip_argmax_workspace_size
+    assert ws(32, 151936) == 32 * 16 * 16  # 16 slices of 9496 logits per row, 16 bytes each
+    assert ws(1, 100) == 0 and ws(4096, 151936) == 0 and ws(0, 10) == 0
