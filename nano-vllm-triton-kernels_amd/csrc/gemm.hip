@@ -496,6 +496,133 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
   }
 }
 
+// gemm_skinny with the operands staged through LDS: the same k steps per wave in the same order and the same MFMA
+// operands (so the same bits), but a round of KR = NW * UR * 32 consecutive k of the block's A rows and W rows is
+// loaded by the whole block with 16-byte loads that run along the rows (32 lanes cover 512 contiguous bytes), and
+// each wave then reads its fragments from LDS. Read straight from memory, a fragment load touches 16 rows x 64 bytes
+// per wave instruction and streams ~31-36 GB/s per CU from L2; row-contiguous loads of the same bytes 55-75 GB/s.
+// Two LDS stages (round r + 1 stored while round r is multiplied, round r + 2 in flight in registers); row pitch
+// KR + 8 elements. Past K the staged chunks are zero, as gemm_skinny's loads are.
+template <int MT, int NCOL, int NW, int UR, bool SILU = false>
+__global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
+  constexpr int NP = SILU ? 2 : 1;
+  constexpr int NT = NCOL >= 16 ? NCOL / 16 : 1;
+  static_assert(NCOL == 8 || NCOL == 16 || NCOL == 32 || NCOL == 64, "output columns per block");
+  constexpr int RA = 16 * MT, RW = NP * NCOL;  // staged rows: A rows, then W rows (product p, column j)
+  constexpr int KR = NW * UR * 32, PITCH = KR + 8, CPR = KR / 8;
+  constexpr int NTH = NW * 64, NCH = (RA + RW) * CPR, CPT = (NCH + NTH - 1) / NTH;
+  constexpr int STAGE = (RA + RW) * PITCH;  // bf16 elements
+  constexpr int RED = NW * NP * NT * MT * 4 * 64;  // floats of the cross-wave reduction (after the last round)
+  constexpr int LDS_BYTES = 4 * STAGE > 4 * RED ? 4 * STAGE : 4 * RED;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+  uint16_t* st = reinterpret_cast<uint16_t*>(lds);
+  const int n0 = blockIdx.x * NCOL, m0 = blockIdx.y * RA;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int fr = lane % 16, fk = (lane / 16) * 8;
+  const int nout = SILU ? g.N / 2 : g.N;
+
+  // chunk c = tid + NTH * i of a round: staged row c / CPR, 16-byte chunk c % CPR of it
+  const uint16_t* src[CPT];
+  int dst[CPT], kof[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = min(tid + NTH * i, NCH - 1), r = c / CPR, kc = c % CPR;
+    if (r < RA) {
+      src[i] = g.a + int64_t(min(m0 + r, g.M - 1)) * g.sam + kc * 8;
+    } else {
+      const int p = (r - RA) / NCOL, j = (r - RA) % NCOL;
+      src[i] = g.w + int64_t(p * nout + min(n0 + j, nout - 1)) * g.swn + kc * 8;
+    }
+    dst[i] = r * PITCH + kc * 8;
+    kof[i] = kc * 8;
+  }
+  auto live = [&](int i) { return NCH % NTH == 0 || i + 1 < CPT || tid + NTH * i < NCH; };
+  u32x4 v[CPT];
+  auto load_round = [&](int r) {
+    const int k0 = r * KR;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      v[i] = (live(i) && k0 + kof[i] < g.K) ? *reinterpret_cast<const u32x4*>(src[i] + k0) : u32x4{0, 0, 0, 0};
+  };
+  auto store_round = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      if (live(i)) *reinterpret_cast<u32x4*>(st + stage * STAGE + dst[i]) = v[i];
+  };
+
+  f32x4_t acc[NP][NT][MT];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[p][j][t] = f32x4_t{};
+  const int rounds = (g.K + KR - 1) / KR;
+  load_round(0);
+  store_round(0);
+  if (rounds > 1) load_round(1);
+  __syncthreads();
+  for (int r = 0; r < rounds; ++r) {
+    const uint16_t* s = st + (r & 1) * STAGE;
+#pragma unroll
+    for (int u = 0; u < UR; ++u) {
+      const int kl = (wave + NW * u) * 32 + fk;  // the wave's k step wave + NW (r UR + u), this lane's 8 k
+      bf16x8_t af[MT], wf[NP][NT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) af[t] = *reinterpret_cast<const bf16x8_t*>(s + (16 * t + fr) * PITCH + kl);
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = NCOL == 8 ? fr % 8 : 16 * j + fr;  // 8 columns: MFMA columns 8..15 repeat 0..7
+          wf[p][j] = *reinterpret_cast<const bf16x8_t*>(s + (RA + p * NCOL + col) * PITCH + kl);
+        }
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+            acc[p][j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], wf[p][j], acc[p][j][t], 0, 0, 0);
+    }
+    if (r + 1 < rounds) {
+      store_round((r + 1) & 1);
+      if (r + 2 < rounds) load_round(r + 2);
+    }
+    __syncthreads();
+  }
+  // cross-wave sum in wave order (the LDS of the stages, no longer read), as gemm_skinny
+  float* red = reinterpret_cast<float*>(lds);
+  auto ridx = [&](int w, int p, int j, int t, int rr, int l) {
+    return ((((w * NP + p) * NT + j) * MT + t) * 4 + rr) * 64 + l;
+  };
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) red[ridx(wave, p, j, t, rr, lane)] = acc[p][j][t][rr];
+  __syncthreads();
+  for (int idx = tid; idx < NT * MT * 256; idx += NTH) {
+    const int j = idx / (MT * 256), t = (idx / 256) % MT, rr = (idx / 64) % 4, l = idx % 64;
+    float sum[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      sum[p] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum[p] += red[ridx(w, p, j, t, rr, l)];
+    }
+    const int m = m0 + t * 16 + 4 * (l / 16) + rr, n = n0 + 16 * j + l % 16;
+    if ((NCOL == 8 && l % 16 >= 8) || m >= g.M || n >= nout) continue;
+    float o = sum[0];
+    if constexpr (SILU) o = silu_bf16(round_bf16(sum[0])) * round_bf16(sum[1]);
+    g.c[int64_t(m) * g.scm + n] = f32_to_bf16(o);
+  }
+}
+
 // ------------------------------------------------------------------------------------------------------------
 // RMSNorm (or Add+RMSNorm) of the A rows fused into the decode GEMM (M <= 32): the norm that precedes a projection
 // (input_layernorm -> qkv, post_attention_layernorm -> gate_up) in the same launch. Every block normalises the
@@ -848,12 +975,16 @@ int launch_mfma_bnm(const MfmaArgs& g, hipStream_t s) {
 // tile per block (grid.y = row tiles) x 16 columns, or x 8 columns. One CU streams at most ~70 GB/s from L2/HBM,
 // and every block reads all of its rows of A (32 x K: twice the W slice of a 16-column block), so narrow outputs
 // (N = 1024: 64 blocks of 32 x 16) need the smaller tiles to reach every CU.
+// 8-column blocks with K >= 2048 (o_proj, down_proj) stage their operands through LDS (gemm_skinny_lds, same bits):
+// o_proj 5.75 -> 4.58 us, down 7.81 -> 6.04 us with the weights from HBM; 16-column blocks and short K measured
+// within 4 % or slower that way (a barrier and an LDS round trip per round for little traffic).
 template <int MT, int NCOL, bool SILU>
 int launch_skinny_tile(const MfmaArgs& g, hipStream_t s) {
   constexpr int NW = 8;
   const int nout = SILU ? g.N / 2 : g.N;
   const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((g.M + 16 * MT - 1) / (16 * MT))), block(NW * 64);
-  if (g.N >= 2048 || NCOL == 8) hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 4, SILU>), grid, block, 0, s, g);
+  if (NCOL == 8 && MT == 1 && g.K >= 2048) hipLaunchKernelGGL((gemm_skinny_lds<1, 8, NW, 4, SILU>), grid, block, 0, s, g);
+  else if (g.N >= 2048 || NCOL == 8) hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 4, SILU>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 8, SILU>), grid, block, 0, s, g);
   return check_launch("matmul");
 }
@@ -863,12 +994,13 @@ int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   constexpr int64_t kBlocks = 256;
   const int64_t nout = SILU ? g.N / 2 : g.N;
   // very wide outputs (the LM head): 64 columns per block, so each block's A reads serve four times the W bytes;
-  // 4 waves of 8 k steps (a quarter of the LDS of 8 waves, so more blocks per CU): 32 x 151936 x 1024 in 74.3 us
-  // vs 81.0 us with 8 waves of 4 (a sweep of 2 / 4 / 8 / 16 waves x 2 / 4 / 8 / 16 steps x 16 / 32 / 64 columns)
+  // 4 waves (a sweep of 2 / 4 / 8 / 16 waves x 2 / 4 / 8 / 16 steps x 16 / 32 / 64 columns picked 4 waves of 8 k
+  // steps for gemm_skinny: 32 x 151936 x 1024 in 73.6 us vs 81.0 us with 8 waves of 4); staged through LDS one
+  // 128-k round at a time (52 KB of LDS, three blocks per CU): 64.3 us (two k steps per wave and round: 86.7 us)
   if constexpr (!SILU)
     if ((nout + 63) / 64 >= 8 * kBlocks) {
       const dim3 grid(unsigned((nout + 63) / 64), unsigned((g.M + 16 * MT - 1) / (16 * MT)));
-      hipLaunchKernelGGL((gemm_skinny<MT, 64, 4, 8, SILU>), grid, dim3(4 * 64), 0, s, g);
+      hipLaunchKernelGGL((gemm_skinny_lds<MT, 64, 4, 1, SILU>), grid, dim3(4 * 64), 0, s, g);
       return check_launch("matmul");
     }
   if ((nout + 15) / 16 >= kBlocks) return launch_skinny_tile<MT, 16, SILU>(g, s);
