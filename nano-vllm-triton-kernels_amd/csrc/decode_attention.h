@@ -61,6 +61,14 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
+// K / V cache rows, read once per launch, with the nontemporal hint: the loads then neither hit nor fill the Infinity
+// Cache, and a batch's cache (~163 MB at batch 32, U[512, 2048] contexts) streams faster from HBM -- per-chunk
+// timestamps show every wave waiting 2-4.5 us for each chunk's loads against 0.6 us of compute, and the launch
+// took 37.0 us with the hint against 41.7 us without (instrumented builds). A second chunk in flight per wave
+// (prefetch) measured slower either way: the chip is at its bandwidth for this pattern while most pairs run.
+__device__ __forceinline__ bf16x8_t load_bf16x8_once(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(p));
+}
 
 // Element offset of token t's row for this kv head in the caches, or -1 if its block is not a valid block.
 // ALIGNED: block_size is a multiple of the chunk, so every token of a chunk lies in the block of the chunk start.
@@ -247,8 +255,8 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
 #pragma unroll
     for (int it = 0; it < PVI; ++it) {
       const int64_t row = row_of(t0 + it * TPI + ts, base, t0);
-      T.k[it] = load_bf16x8(row >= 0 ? g.kc + row + 8 * dg : g.q);
-      T.v[it] = load_bf16x8(row >= 0 ? g.vc + row + 8 * dg : g.q);
+      T.k[it] = load_bf16x8_once(row >= 0 ? g.kc + row + 8 * dg : g.q);
+      T.v[it] = load_bf16x8_once(row >= 0 ? g.vc + row + 8 * dg : g.q);
     }
   };
   constexpr float kLazy = 8.0f;
@@ -334,8 +342,7 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
   };
 
   // The wave's chunks are first, first + 8, ... (issuing two chunks' loads before computing them, or prefetching
-  // the next chunk during the current one, measured no faster: a read-only kernel with this access pattern and
-  // no compute takes ~35 us where this one takes ~43 us for 163 MB of K/V).
+  // the next chunk during the current one, measured no faster).
   for (int ch = tok_begin / kChunk + wave; ch < ch_end; ch += NWV) {
     Tile A;
     load_tile(A, ch);
