@@ -114,6 +114,27 @@ def test_rows_do_not_depend_on_the_tile_choice(layer):
 
 
 @pytest.mark.parametrize("M", [1, 17, 32])
+@pytest.mark.parametrize("K", [1024, 2048, 3072])
+def test_decode_column_tilings_agree_bitwise(M, K):
+    """M <= 32: the 8-wave block tilings sum a column in the same k order, so a column has the same bits in an
+    8-column block (staged through LDS from K = 2048 on, N = 1024) and in a 16-column block with fragments loaded
+    straight from memory (N = 4096); the 4-wave 64-column blocks of LM-head-wide outputs (staged through LDS) agree
+    with each other whatever the output width (151 936 = the Qwen3 vocabulary, 131 176 = 2049 blocks and a ragged one) and with the
+    fp64 product."""
+    g = torch.Generator(DEV).manual_seed(M * 131 + K)
+    a = (torch.randn(M, K, generator=g, device=DEV) / math.sqrt(K)).to(torch.bfloat16)
+    w = torch.randn(151936, K, generator=g, device=DEV).to(torch.bfloat16)
+    mid = matmul(a, w[:4096].t())
+    narrow = matmul(a, w[:1024].t())
+    assert torch.equal(mid[:, :1024], narrow)
+    wide = matmul(a, w.t())
+    wide2 = matmul(a, w[:131176].t())
+    assert torch.equal(wide[:, :131176], wide2)
+    ref = oracle.matmul_fp64(a.cpu(), w[:4096].cpu().t())
+    torch.testing.assert_close(wide[:, :4096].cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("M", [1, 17, 32])
 def test_decode_tiles_wide_and_narrow_outputs(M):
     """M <= 32 picks its block tile by the output width: 64 columns for an LM-head-wide output (151 936 = the Qwen3
     vocabulary, not a multiple of 64), one 16-row tile x 8 columns for N = 1024, and the ragged tails of both."""
