@@ -114,11 +114,11 @@ def test_rows_do_not_depend_on_the_tile_choice(layer):
 
 
 @pytest.mark.parametrize("M", [1, 17, 32])
-@pytest.mark.parametrize("K", [1024, 2048, 3072])
+@pytest.mark.parametrize("K", [1024, 2048, 2056, 3072, 4104])
 def test_decode_column_tilings_agree_bitwise(M, K):
     """M <= 32: the 8-wave block tilings sum a column in the same k order, so a column has the same bits in an
-    8-column block (staged through LDS from K = 2048 on, N = 1024) and in a 16-column block with fragments loaded
-    straight from memory (N = 4096); the 4-wave 64-column blocks of LM-head-wide outputs (staged through LDS) agree
+    8-column block (staged through LDS from K = 2048 on, N = 1024; K = 2056 / 4104 end in a partial round) and in a
+    16-column block with fragments loaded straight from memory (N = 4096); the 4-wave 64-column blocks of LM-head-wide outputs (staged through LDS) agree
     with each other whatever the output width (151 936 = the Qwen3 vocabulary, 131 176 = 2049 blocks and a ragged one) and with the
     fp64 product."""
     g = torch.Generator(DEV).manual_seed(M * 131 + K)
