@@ -140,9 +140,14 @@ int nvhip_store_kvcache(void* k_cache, void* v_cache, const void* key, const voi
  *   context_lens: [num_seqs] int32 cache tokens per sequence, including the q_len new ones (0 = padding: zero
  *   output). Query i sees cache tokens < context_len - q_len + i + 1 when causal, all context_len otherwise.
  *   Blocks outside [0, num_blocks) are skipped. D: 64, 128, 256; (Hq / Hkv) * q_len <= 16 (8 for D = 256).
- *   workspace: device memory of at least nvhip_paged_decode_attention_workspace_size(...) bytes (contents need no
- *   initialisation; used by this call only) lets long contexts be split over several blocks and merged by a second
- *   kernel; NULL (or too small) runs one block per (sequence, kv head).
+ *   workspace: device memory of at least nvhip_paged_decode_attention_workspace_size(...) bytes, 256-byte
+ *   aligned, ZERO-FILLED before its first use (its first 2 KiB are per-(sequence, kv head) counters; every call
+ *   leaves them zero again, so a workspace is zeroed once and kept; calls that share it must be ordered on one
+ *   stream). With it, fewer (sequence, kv head) pairs than CUs split each context over several blocks, and 256 to
+ *   512 pairs of at most 64 sequences are balanced by length (the longest and shortest sequences paired, the
+ *   long pair's tail taken by the short pair's block); the blocks of a split pair merge their (max, sum, O)
+ *   records themselves, in split order (the last to finish, found with a device-scope counter). NULL (or too
+ *   small) runs one block per (sequence, kv head).
  * Numerics: fp32 scores and softmax (exp2 with the scale folded in), fp32 P*V accumulation, bf16 output.
  */
 int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_cache, const void* v_cache,
@@ -154,15 +159,14 @@ int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_ca
                                       void* stream);
 
 /*
- * nvhip_paged_decode_attention_bf16 without a workspace argument and without any allocation: the context-split
- * records go to a device array of this library (9 MiB per GPU, held until the process ends; its address on the
- * current device is looked up once per device with hipGetSymbolAddress). No counterpart in the reference: for
- * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). Same arguments, split policy and results as nvhip_paged_decode_attention_bf16 given a workspace
- * of nvhip_paged_decode_attention_workspace_size(...) bytes; a need beyond the array is refused (NVHIP_EINVAL; the
- * split policy never asks for more). All calls on one GPU share the array: calls that overlap in time on one GPU
- * (different streams without ordering) race on it. The records need no initialisation (every block writes its own
- * before the merge kernel reads it).
+ * nvhip_paged_decode_attention_bf16 without a workspace argument and without any allocation: the pair counters and
+ * split records go to a device array of this library (18 MiB per GPU, zero at load, held until the process ends;
+ * its address on the current device is looked up once per device with hipGetSymbolAddress). No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, plan and results as nvhip_paged_decode_attention_bf16 given a
+ * zero-filled workspace of nvhip_paged_decode_attention_workspace_size(...) bytes; a need beyond the array is
+ * refused (NVHIP_EINVAL; the plan never asks for more). All calls on one GPU share the array: calls that overlap in
+ * time on one GPU (different streams without ordering) race on it. Every call leaves the counters zero.
  */
 int nvhip_paged_decode_attention_bf16_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
                                               const int32_t* block_table, const int32_t* context_lens,
@@ -211,8 +215,9 @@ int64_t nvhip_prefill_attention_workspace_size(int64_t num_seqs, int64_t max_seq
                                                int64_t Hq, int64_t Hkv, int64_t D, int64_t total_q);
 
 /*
- * Bytes of workspace nvhip_paged_decode_attention_bf16 uses for these sizes (0: it does not split). Host-only, no
- * GPU work. An addition of this library (the reference has no workspace: flash-attn allocates its own).
+ * Bytes of workspace nvhip_paged_decode_attention_bf16 uses for these sizes (0: one block per (sequence, kv head)).
+ * Host-only, no GPU work. An addition of this library (the reference has no workspace: flash-attn allocates its
+ * own).
  */
 int64_t nvhip_paged_decode_attention_workspace_size(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv,
                                                     int64_t D, int64_t block_size, int64_t max_blocks);
@@ -249,7 +254,8 @@ int64_t nvhip_matmul_add_rms_norm_workspace_size(int64_t M, int64_t N, int64_t K
  * block_size)) before it reads the cache; the output is bitwise that of the two calls when slot_mapping[b] is
  * the slot of sequence b's position context_lens[b] - 1 in its block table (as every decode step builds it). A slot
  * outside that layout is still written, but ordered before the reads of the writing block only: another block that
- * reads it in the same launch (another context split of the pair, another sequence) may see the old row.
+ * reads it in the same launch (another context split or balanced piece of the pair, another sequence) may see the
+ * old row.
  *   q [num_seqs, Hq, D], k, v [num_seqs, Hkv, D]: the raw rows of the qkv projection (token strides q_stride,
  *   k_stride, v_stride, multiples of 8; heads contiguous; 16-byte aligned). positions int64, slot_mapping int32
  *   [num_seqs]; q_weight, k_weight [D]; cos_sin [max_pos, cos_sin_stride] fp32 (cos | sin); caches, block_table,

@@ -297,7 +297,16 @@ __device__ __forceinline__ void norm_rope16(const float* x1, const float* x2, fl
 // Element d of row r of one (sequence, kv head) from its context splits' records (fp32 max, sum, two more, O[D] ...
 // at rec0 + s * step for split s, the (max, sum) pair first): O = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),
 // M = max_s m_s, merged in split order; 0 for a row no split saw (M = -inf). Up to 4 splits' loads issue at once.
+// DEVICE_SCOPE: the records were written by other blocks of the running kernel (possibly on other XCDs, whose L2s
+// are not coherent with this one): read with device-scope loads (sc1), which do not return this XCD's L2 copy.
+template <bool DEVICE_SCOPE = false>
 __device__ __forceinline__ float merge_splits(const float* rec0, int64_t step, int splits, int d_off) {
+  auto ld = [](const float* p) -> float {
+    if constexpr (DEVICE_SCOPE)
+      return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      return *p;
+  };
   float num = 0.0f, den = 0.0f;
   if (splits <= 4) {
     float m[4], l[4], o[4];
@@ -305,9 +314,9 @@ __device__ __forceinline__ float merge_splits(const float* rec0, int64_t step, i
     for (int u = 0; u < 4; ++u) {
       m[u] = -INFINITY, l[u] = o[u] = 0.0f;
       if (u < splits) {
-        m[u] = rec0[u * step];
-        l[u] = rec0[u * step + 1];
-        o[u] = rec0[u * step + d_off];
+        m[u] = ld(rec0 + u * step);
+        l[u] = ld(rec0 + u * step + 1);
+        o[u] = ld(rec0 + u * step + d_off);
       }
     }
     float M = -INFINITY;
@@ -324,12 +333,12 @@ __device__ __forceinline__ float merge_splits(const float* rec0, int64_t step, i
     }
   } else {
     float M = -INFINITY;
-    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, rec0[sp * step]);
+    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, ld(rec0 + sp * step));
     if (M != -INFINITY) {
       for (int sp = 0; sp < splits; ++sp) {
-        const float f = exp2f(rec0[sp * step] - M);
-        num = __builtin_fmaf(rec0[sp * step + d_off], f, num);
-        den = __builtin_fmaf(rec0[sp * step + 1], f, den);
+        const float f = exp2f(ld(rec0 + sp * step) - M);
+        num = __builtin_fmaf(ld(rec0 + sp * step + d_off), f, num);
+        den = __builtin_fmaf(ld(rec0 + sp * step + 1), f, den);
       }
     }
   }

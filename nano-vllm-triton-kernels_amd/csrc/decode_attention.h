@@ -31,7 +31,8 @@ struct DecodeArgs {
   int causal;
   int splits;     // context splits per (sequence, kv head): blocks s = 0 .. splits-1 take tokens
   int split_len;  // [s * split_len, (s + 1) * split_len); a multiple of kChunk * kWaves (so of kChunk * waves)
-  float* ws;      // splits > 1: [num_seqs, Hkv, splits, RP, 2 + D] fp32 records (max, sum, O) of each block
+  float* ws;      // split pairs: fp32 records (max, sum, O[D]) per row, rec_stride floats per (pair, split) block
+                  // of RP rows at ws + (pair * rec_splits + split) * rec_stride
   // varlen (the short sequences of a paged prefill call, splits = 1): sequence b's queries are rows cu_q[b] ..
   // cu_q[b+1]-1 of q and out and its context is cu_k[b+1] - cu_k[b] keys; a sequence with no queries or more
   // than q_len is left alone (the prefill kernel takes it). Null: q_len queries per sequence, ctx_lens.
@@ -52,7 +53,24 @@ struct DecodeArgs {
   const float* cos_sin;
   int64_t cs_st, max_pos, num_slots;
   float inv_d, eps;
+  int rec_splits;      // record blocks per pair
+  int64_t rec_stride;  // floats per record block (>= RP * (2 + D))
+  // counters != null (ctx_lens calls): the blocks of a split pair merge their records themselves -- each writes
+  // its record through to memory, waits for the stores, and bumps the pair's counter; the block that brings it to
+  // the pair's split count reads every record with device-scope loads, merges them in split order (the combine
+  // kernel's arithmetic) and sets the counter back to 0. The counters are zero between calls.
+  uint32_t* counters;
+  int num_seqs;
+  int balance;  // pieces from balance_pieces (length-aware) instead of splits x split_len
 };
+
+// A block's share of one (sequence, kv head) pair: tokens [tok_begin, min(ctx, tok_stop)), split `split` of the
+// pair's `nsplit` (nsplit > 1: the pieces' records are merged).
+struct Piece {
+  int pair, split, nsplit, tok_begin, tok_stop;
+};
+
+constexpr int kMinTail = 128;  // a long pair's tail shorter than this stays with its own block
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -80,6 +98,40 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 }
 
 
+// Balanced pieces (decode calls of 2 .. 64 sequences with context lengths): the sequences are ranked by context
+// length (longest first, ties by index) and rank r < n / 2 is paired with rank n - 1 - r. For each kv head the long
+// sequence's pair is cut where both blocks get the same work: the long pair's block takes [0, cut), the short
+// pair's block takes [cut, ctx_long) and then its own whole context, so that every block of the launch streams
+// about (ctx_long + ctx_short) / 2 tokens from the start -- instead of the longest pairs streaming alone at the end
+// while the CUs of the short ones idle. Cuts are whole 32-token chunks; a tail under kMinTail tokens is not cut.
+// Fills pc with block bid's pieces (the tail first) and returns their count; every wave computes the same plan
+// (one context length per lane).
+__device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piece* pc) {
+  const int lane = threadIdx.x % 64, n = g.num_seqs, cap = g.max_blocks * g.bs;
+  const int c = lane < n ? min(max(g.ctx_lens[lane], 0), cap) : -1;
+  int rank = 0;  // lanes >= n rank after every sequence
+  for (int j = 0; j < 64; ++j) {
+    const int cj = __builtin_amdgcn_readlane(c, j);
+    rank += (cj > c || (cj == c && j < lane)) ? 1 : 0;
+  }
+  const int b = bid / g.Hkv, h = bid % g.Hkv;
+  const int rb = __builtin_amdgcn_readlane(rank, b), rp = n - 1 - rb;
+  pc[0] = Piece{bid, 0, 1, 0, INT32_MAX};
+  if (rb == rp) return 1;  // the median of an odd batch
+  const int bp = __ffsll((unsigned long long)__ballot(rank == rp)) - 1;
+  const int cb = __builtin_amdgcn_readlane(c, b), cp = __builtin_amdgcn_readlane(c, bp);
+  const int c_long = rb < rp ? cb : cp, c_short = rb < rp ? cp : cb;
+  const int cut = min(c_long, (((c_long + c_short + 1) / 2) + kChunk - 1) / kChunk * kChunk);
+  if (c_long - cut < kMinTail) return 1;
+  if (rb < rp) {  // the long pair: its head
+    pc[0].nsplit = 2, pc[0].tok_stop = cut;
+    return 1;
+  }
+  pc[1] = pc[0];  // the short pair: the long pair's tail, then its own context
+  pc[0] = Piece{bp * g.Hkv + h, 1, 2, cut, INT32_MAX};
+  return 2;
+}
+
 // Bytes of LDS decode_block uses: every wave's K and V chunk (or, afterwards, its partial O) and the waves' row max
 // and sum.
 __host__ __device__ constexpr int decode_lds_bytes(int D, int RP, bool) {
@@ -88,7 +140,7 @@ __host__ __device__ constexpr int decode_lds_bytes(int D, int RP, bool) {
 }
 
 template <int D, int RP, bool ALIGNED, bool FUSE = false>
-__device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid, unsigned char* lds) {
+__device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& pc, unsigned char* lds) {
   constexpr int NWV = block_waves(D);
   constexpr int KC = D / 32;         // 32-wide dim chunks of a K row (MFMA k steps of Q.K)
   constexpr int LPT = D / 8;         // lanes per V row in the row layout
@@ -108,7 +160,7 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
   bool fresh_here = false;  // FUSE: this block's token range holds the new token (wave-uniform)
   u32x4 na = {}, nb = {};    // FUSE: this lane's 8 + 8 elements of the new key (lanes < D/16) or value row
 
-  const int split = bid % g.splits, pair = bid / g.splits;
+  const int pair = pc.pair, split = pc.split, nsplit = pc.nsplit, tok_begin = pc.tok_begin, tok_stop = pc.tok_stop;
   const int b = pair / g.Hkv, kvh = pair % g.Hkv;
   const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   int q0 = b * g.q_len, lq = g.q_len, ctx;  // the sequence's first query row, its queries and context length
@@ -122,7 +174,7 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
   }
   const int rows = g.G * lq;
   const int32_t* bt_row = g.bt + int64_t(b) * g.max_blocks;
-  const int tok_begin = split * g.split_len, blk0 = tok_begin / g.bs;
+  const int blk0 = tok_begin / g.bs;
   // issued together: this split's first 64 block-table entries (one per lane) and the Q rows
   const int bt_lane = blk0 + lane < g.max_blocks ? bt_row[blk0 + lane] : -1;
 
@@ -176,8 +228,7 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
     }
     // the new key (lanes 0 .. D/16-1 of wave 0, the fused norm's own lane layout) and value (the next D/16 lanes)
     const int32_t slot = g.slots[b];
-    const bool writer = ctx > 0 ? (split * g.split_len <= ctx - 1 && ctx - 1 < split * g.split_len + g.split_len)
-                                : split == 0;
+    const bool writer = ctx > 0 ? (tok_begin <= ctx - 1 && ctx - 1 < tok_stop) : split == 0;
     const bool store = writer && slot >= 0 && slot < g.num_slots;
     // the new rows stand in for what the chunk loads read at position ctx - 1 when that is the slot they go to (a
     // decode step); otherwise (inconsistent slot, clamped context) they are written before any wave reads
@@ -227,7 +278,7 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
   const int h4 = lane / 16, l16 = lane % 16;
   uint16_t* vs = reinterpret_cast<uint16_t*>(smem) + wave * kChunk * (VPW + KPW);  // this wave's V chunk
   uint16_t* ks = vs + kChunk * VPW;                                                 // and K chunk
-  const int tok_end = min(ctx, tok_begin + g.split_len);
+  const int tok_end = min(ctx, tok_stop);
   const int ch_end = (tok_end + kChunk - 1) / kChunk;
 
   // A chunk's K and V fragments (registers) and which of its tokens are valid. Every load instruction is issued
@@ -379,19 +430,68 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
         den = __builtin_fmaf(red_l[w][r], f, den);
       }
     }
-    if (g.splits > 1) {  // this block's record; merged by paged_decode_combine
-      float* rec = g.ws + ((int64_t(pair) * g.splits + split) * RP + r) * (2 + D);
-      if (d == 0) {
-        rec[0] = M;
-        rec[1] = den;
+    if (nsplit > 1) {  // this block's record, merged by paged_decode_combine or below
+      float* rec = g.ws + (int64_t(pair) * g.rec_splits + split) * g.rec_stride + r * (2 + D);
+      if (g.counters != nullptr) {  // written through the L2 (sc1): the merging block may sit on another XCD
+        if (d == 0) {
+          __hip_atomic_store(rec, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(rec + 1, den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __hip_atomic_store(rec + 2 + d, num, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (d == 0) {
+          rec[0] = M;
+          rec[1] = den;
+        }
+        rec[2 + d] = num;
       }
-      rec[2 + d] = num;
       continue;
     }
     const float o = den > 0.0f ? num / den : 0.0f;
     const int i = r / g.G, hh = r % g.G;
     g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
   }
+  if (nsplit == 1 || g.counters == nullptr) return;
+  // The last block of the pair merges. Every wave waits for its record stores to complete (written through to
+  // memory) before the barrier; the counter is a device-scope atomic; the merging block reads the records with
+  // device-scope loads after its atomic returned. No L2 write-back or invalidate is needed.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int* flag = reinterpret_cast<int*>(red_m);  // free: every thread is past the merge loop above
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(g.counters + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == uint32_t(nsplit - 1);
+    if (last) __hip_atomic_store(g.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  if (!*flag) return;
+  for (int idx = threadIdx.x; idx < rows * D; idx += NWV * 64) {
+    const int r = idx / D, d = idx % D;
+    const float* rec = g.ws + int64_t(pair) * g.rec_splits * g.rec_stride + r * (2 + D);
+    const float o = merge_splits<true>(rec, g.rec_stride, nsplit, 2 + d);
+    const int i = r / g.G, hh = r % g.G;
+    g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
+  }
+}
+
+// Block bid: split bid % splits of pair bid / splits, or (balance) its one or two balanced pieces, one after the
+// other (a barrier between them: the second piece's chunks reuse the LDS of the first's merge).
+template <int D, int RP, bool ALIGNED, bool FUSE = false>
+__device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid, unsigned char* lds) {
+  if (g.balance) {
+    Piece pc[2];
+    const int n = balance_pieces(g, bid, pc);
+    decode_piece<D, RP, ALIGNED, FUSE>(g, pc[0], lds);
+    if (n > 1) {
+      __syncthreads();
+      decode_piece<D, RP, ALIGNED, FUSE>(g, pc[1], lds);
+    }
+    return;
+  }
+  const int split = bid % g.splits;
+  decode_piece<D, RP, ALIGNED, FUSE>(g, Piece{bid / g.splits, split, g.splits, split * g.split_len,
+                                              split * g.split_len + g.split_len}, lds);
 }
 
 }  // namespace

@@ -33,9 +33,20 @@
 // Varlen: a paged prefill call (prefill_attention.hip) hands its sequences with few queries (<= 16 / G each, e.g.
 // the decode requests of a mixed step) to this kernel, with per-sequence query rows and context lengths from
 // cu_seqlens; the prefill kernel's 128-query tiles would spend a whole tile's work per key on them.
-// Small batches: with a caller workspace the context of each (sequence, kv head) is split over several blocks
-// (whole 256-token rounds) when there are fewer pairs than CUs; each block writes its merged (max, sum, O) record
-// and a second kernel merges the records in split order. Without a workspace one block covers the whole context.
+// Work split (with a caller workspace): with fewer pairs than CUs the context of each (sequence, kv head) is split
+// over several blocks (whole 256-token rounds); with 256 to 512 pairs of at most 64 sequences the batch is
+// balanced by length -- the longest and shortest sequences paired, the long pair's tail run by the short pair's
+// block before its own context -- because one block per pair leaves the longest pairs streaming alone at the end
+// (batch 32, contexts U[512, 2048]: 36.6 -> 34.8 us). The blocks of a split pair each write their merged (max,
+// sum, O) record through the L2 (sc1 stores), wait for the stores and bump the pair's counter (a device-scope
+// atomic); the block that completes the count reads the records with device-scope loads and merges them in split
+// order, so no second launch is needed (the XCDs' L2s are not coherent with each other, and agent-scope fences --
+// a write-back and an invalidate of the whole L2 -- measured 30-400 us per call; the stores, atomic and loads of
+// this hand-off measured ~2.6 us at the end of the pair). Without a workspace one block covers the whole context.
+// Per-block timestamps of the balanced launch show the blocks' work equal to +-8 % but their loop times spread
+// 3.6-6.3 us per 256 tokens: under full load the pairs of kv heads 1 and 5 stream ~25 % slower (their 256-byte
+// slices of the 2 KiB token rows sit on busier HBM channels; with kv heads and XCDs decoupled the difference
+// follows the head), which a static balance cannot see.
 // Tokens past the context, blocks outside [0, num_blocks) and rows past a query's causal limit take no part (their
 // K/V are not read; p = 0).
 #include <algorithm>
@@ -67,20 +78,31 @@ __global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) 
   const int rows = g.G * lq;
   for (int idx = threadIdx.x; idx < rows * D; idx += 256) {
     const int r = idx / D, d = idx % D;
-    const float* rec = g.ws + (int64_t(pair) * g.splits * RP + r) * (2 + D);
-    const float o = merge_splits(rec, int64_t(RP) * (2 + D), g.splits, 2 + d);
+    const float* rec = g.ws + int64_t(pair) * g.rec_splits * g.rec_stride + r * (2 + D);
+    const float o = merge_splits(rec, g.rec_stride, g.splits, 2 + d);
     const int i = r / g.G, hh = r % g.G;
     g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
   }
 }
 
+// Floats per record block of RP rows: whole 128-byte lines when the blocks merge in the kernel (each line is
+// written by one block).
+int64_t record_stride(int64_t RP, int64_t D, bool in_kernel) {
+  const int64_t f = RP * (2 + D);
+  return in_kernel ? (f + 31) / 32 * 32 : f;
+}
+
 template <int D, int RP, bool FUSE = false>
-int launch_decode(const DecodeArgs& g, int64_t num_seqs, hipStream_t s) {
-  const dim3 grid(unsigned(num_seqs * g.Hkv * g.splits)), block(block_waves(D) * 64);
+int launch_decode(const DecodeArgs& args, int64_t num_seqs, hipStream_t s) {
+  DecodeArgs g = args;
+  g.rec_splits = g.balance ? 2 : g.splits;
+  g.rec_stride = record_stride(RP, D, g.counters != nullptr);
+  const int64_t blocks = num_seqs * g.Hkv * g.splits;  // balance: one block per pair (splits = 1)
+  const dim3 grid(static_cast<unsigned>(blocks)), block(block_waves(D) * 64);
   if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true, FUSE>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((paged_decode_kernel<D, RP, false, FUSE>), grid, block, 0, s, g);
   if (int rc = check_launch("paged_decode_attention")) return rc;
-  if (g.splits == 1) return NVHIP_OK;
+  if (g.splits == 1 || g.counters != nullptr) return NVHIP_OK;
   hipLaunchKernelGGL((paged_decode_combine<D, RP>), dim3(unsigned(num_seqs * g.Hkv)), dim3(256), 0, s, g);
   return check_launch("paged_decode_attention (combine)");
 }
@@ -111,11 +133,47 @@ void split_policy(int64_t num_seqs, int64_t Hkv, int64_t max_ctx, int& splits, i
   split_len = int(std::min<int64_t>(len, INT32_MAX / 2));
 }
 
+// Decode calls with context lengths (not varlen): fewer pairs than CUs -> splits x split_len (split_policy); 256 to
+// 512 pairs of at most 64 sequences -> balance (length-aware: long and short sequences paired, the long pair's
+// tail taken by the short pair's block, balance_pieces);
+// either way the blocks of a split pair merge their records in the kernel. Workspace: 512 uint32 counters, one per
+// pair (zero between calls; a fixed region, so that one workspace can serve calls of any shape), then the record
+// blocks.
+constexpr int64_t kBalanceMaxPairs = 512, kCounterBytes = kBalanceMaxPairs * 4;
+struct DecodePlan {
+  int splits = 1, split_len = 0, balance = 0;
+  int64_t counter_bytes = 0, bytes = 0;
+};
+DecodePlan decode_plan(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_ctx) {
+  DecodePlan p;
+  split_policy(num_seqs, Hkv, max_ctx, p.splits, p.split_len);
+  const int64_t pairs = num_seqs * Hkv, round = kChunk * block_waves(int(D));
+  int64_t blocks = 0;
+  if (p.splits > 1) {
+    blocks = pairs * p.splits;
+  } else if (num_seqs >= 2 && num_seqs <= 64 && pairs <= kBalanceMaxPairs && max_ctx >= 2 * round) {
+    p.balance = 1;
+    blocks = pairs * 2;
+  }
+  if (blocks == 0) return p;
+  p.counter_bytes = kCounterBytes;  // splits x split_len: fewer than 256 pairs; balance: at most 512
+  p.bytes = p.counter_bytes + blocks * record_stride(rows_padded((Hq / Hkv) * q_len), D, true) * int64_t(sizeof(float));
+  return p;
+}
 int64_t workspace_bytes(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_ctx) {
-  int splits, split_len;
-  split_policy(num_seqs, Hkv, max_ctx, splits, split_len);
-  if (splits <= 1) return 0;
-  return num_seqs * Hkv * splits * rows_padded((Hq / Hkv) * q_len) * (2 + D) * int64_t(sizeof(float));
+  return decode_plan(num_seqs, q_len, Hq, Hkv, D, max_ctx).bytes;
+}
+// Points g at the workspace when it is large enough (counters first, records after them).
+int use_workspace(DecodeArgs& g, const DecodePlan& p, int64_t num_seqs, void* workspace, int64_t workspace_size,
+                  const char* what) {
+  if (p.bytes == 0 || workspace == nullptr || workspace_size < p.bytes) return NVHIP_OK;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return invalid(std::string(what) + ": workspace must be 256-byte aligned");
+  g.splits = p.splits, g.split_len = p.split_len, g.balance = p.balance;
+  g.counters = static_cast<uint32_t*>(workspace);
+  g.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes);
+  g.num_seqs = int(num_seqs);
+  return NVHIP_OK;
 }
 
 }  // namespace
@@ -217,15 +275,10 @@ extern "C" int nvhip_paged_decode_attention_bf16(void* out, const void* q, const
                nullptr,
                nullptr,
                nullptr};
-  // split the context over several blocks when the caller gave a large enough workspace
-  const int64_t need = workspace_bytes(num_seqs, q_len, Hq, Hkv, D, max_blocks * block_size);
-  if (need > 0 && workspace && workspace_size >= need) {
-    if (reinterpret_cast<uintptr_t>(workspace) % alignof(float) != 0)
-      return invalid("paged_decode_attention: workspace must be 4-byte aligned");
-    split_policy(num_seqs, Hkv, max_blocks * block_size, g.splits, g.split_len);
-    g.ws = static_cast<float*>(workspace);
-  }
-  if (num_seqs * Hkv * g.splits > INT32_MAX) return invalid("paged_decode_attention: size too large");
+  // split contexts over several blocks when the caller gave a large enough workspace
+  const DecodePlan plan = decode_plan(num_seqs, q_len, Hq, Hkv, D, max_blocks * block_size);
+  if (int rc = use_workspace(g, plan, num_seqs, workspace, workspace_size, "paged_decode_attention")) return rc;
+  if (num_seqs * Hkv * g.splits * 2 > INT32_MAX) return invalid("paged_decode_attention: size too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (D) {
     case 64: return launch_decode_rows<64>(g, num_seqs, int(rows), s);
@@ -282,14 +335,10 @@ extern "C" int nvhip_qk_norm_rope_kv_decode_attention_bf16(
   g.q_w = static_cast<const uint16_t*>(q_weight), g.k_w = static_cast<const uint16_t*>(k_weight);
   g.cos_sin = cos_sin, g.cs_st = cos_sin_stride, g.max_pos = max_pos, g.num_slots = num_blocks * block_size;
   g.inv_d = 1.0f / float(D), g.eps = eps;
-  const int64_t need = workspace_bytes(num_seqs, 1, Hq, Hkv, D, max_blocks * block_size);
-  if (need > 0 && workspace && workspace_size >= need) {
-    if (reinterpret_cast<uintptr_t>(workspace) % alignof(float) != 0)
-      return invalid("qk_norm_rope_kv_decode_attention: workspace must be 4-byte aligned");
-    split_policy(num_seqs, Hkv, max_blocks * block_size, g.splits, g.split_len);
-    g.ws = static_cast<float*>(workspace);
-  }
-  if (num_seqs * Hkv * g.splits > INT32_MAX) return invalid("qk_norm_rope_kv_decode_attention: size too large");
+  const DecodePlan plan = decode_plan(num_seqs, 1, Hq, Hkv, D, max_blocks * block_size);
+  if (int rc = use_workspace(g, plan, num_seqs, workspace, workspace_size, "qk_norm_rope_kv_decode_attention"))
+    return rc;
+  if (num_seqs * Hkv * g.splits * 2 > INT32_MAX) return invalid("qk_norm_rope_kv_decode_attention: size too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows = g.G;
   if (D == 64) {
@@ -307,15 +356,16 @@ extern "C" int nvhip_qk_norm_rope_kv_decode_attention_bf16(
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Allocation-free variant: the split records live in `scratch`, a file-scope device array (each GPU the library
-// runs on holds its own copy until the process ends). The policy above makes fewer than 512 (sequence, kv head,
-// split) blocks whenever it splits, each with at most 16 rows of (2 + D <= 258) fp32, so kScratchBytes (9 MiB)
-// covers every size it can choose; a larger need is refused. In host code `scratch` is only a stand-in for the
+// Allocation-free variant: the pair counters and split records live in `scratch`, a file-scope device array (each
+// GPU the library runs on holds its own copy until the process ends; zero at load, and every call leaves its
+// counters zero). The plan above makes at most 1024 record blocks (fewer than 512 with splits x split_len, 2 per
+// pair of at most 512 pairs when balancing), each of at most 16 rows of (2 + D <= 258) fp32 (16.1 KiB), after at
+// most 2 KiB of counters, so kScratchBytes (18 MiB) covers every size it can choose; a larger need is refused. In host code `scratch` is only a stand-in for the
 // symbol: its device address on the current GPU comes from hipGetSymbolAddress, looked up once per device on the
 // first call made with that device current, and only that address reaches the kernels.
 namespace nvhip {
 namespace {
-constexpr int64_t kScratchBytes = int64_t(9) << 20;
+constexpr int64_t kScratchBytes = int64_t(18) << 20;
 constexpr int kScratchDevices = 64;
 }  // namespace
 }  // namespace nvhip

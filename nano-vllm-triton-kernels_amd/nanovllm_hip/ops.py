@@ -177,6 +177,22 @@ def _matmul_fake(a, b, input_precision):
 
 # ------------------------------------------------------------------ paged decode attention
 
+# The decode attention's workspaces: the kernel's per-pair counters must be zero before a call and every call leaves
+# them zero, so a workspace is zero-filled once and kept, one per (device, stream) -- calls on one stream never
+# overlap. A workspace is never freed: a captured graph keeps using its address (a larger need adds a new one).
+_DECODE_WS = {}
+
+
+def _decode_workspace(device, nbytes):
+    if nbytes <= 0:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    held = _DECODE_WS.setdefault(key, [])
+    if not held or held[-1].numel() < nbytes:
+        held.append(torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device))
+    return held[-1]
+
+
 def _paged_decode_attention_impl(q, k_cache, v_cache, block_table, context_lens, q_len, scale, causal):
     T, Hq, D = q.shape
     num_blocks, block_size, Hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
@@ -184,7 +200,7 @@ def _paged_decode_attention_impl(q, k_cache, v_cache, block_table, context_lens,
     out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
     lib = _lib.lib()
     ws_bytes = lib.nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, Hkv, D, block_size, max_blocks)
-    ws = torch.empty((max(ws_bytes, 0) + 3) // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    ws = _decode_workspace(q.device, ws_bytes)
     status = lib.nvhip_paged_decode_attention_bf16(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
         context_lens.data_ptr(), num_seqs, q_len, Hq, Hkv, D, block_size, num_blocks, max_blocks,
@@ -303,7 +319,7 @@ def _qk_norm_rope_kv_decode_attention_impl(q, k, v, positions, q_w, k_w, eps, co
     out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     lib = _lib.lib()
     ws_bytes = lib.nvhip_paged_decode_attention_workspace_size(B, 1, Hq, Hkv, D, block_size, max_blocks)
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    ws = _decode_workspace(q.device, ws_bytes)
     cs = cos_sin.reshape(cos_sin.shape[0], -1)
     status = lib.nvhip_qk_norm_rope_kv_decode_attention_bf16(
         out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),

@@ -53,3 +53,27 @@ def random_block_table_slots(T, num_blocks, g, num_seqs=4, pad_frac=0.0):
         pad = torch.rand(T, generator=g) < pad_frac
         slots[pad] = -1
     return slots, positions
+
+
+def paged_decode_abi(q, kc, vc, lens, bt, scale, causal, workspace):
+    """Calls nvhip_paged_decode_attention_bf16 directly: workspace False -> one block per (sequence, kv head);
+    True -> a zero-filled workspace of the size the entry point asks for (its context splits, or the length-aware
+    balance of 256 .. 512 pairs). Returns the output and the workspace size."""
+    from nanovllm_hip import _lib
+    num_seqs, q_len, Hq, D = q.shape
+    qf = q.reshape(num_seqs * q_len, Hq, D)
+    out = torch.empty_like(qf)
+    lib = _lib.lib()
+    need = lib.nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, kc.shape[2], D, kc.shape[1],
+                                                           bt.shape[1])
+    # zero-filled: the entry point's per-pair counters must be zero before a call (each call leaves them zero)
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=q.device) if workspace else None
+    status = lib.nvhip_paged_decode_attention_bf16(
+        out.data_ptr(), qf.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), lens.data_ptr(), num_seqs,
+        q_len, Hq, kc.shape[2], D, kc.shape[1], kc.shape[0], bt.shape[1], qf.stride(0), qf.stride(1),
+        out.stride(0), out.stride(1), scale, int(causal), ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, _lib.stream_of(q))
+    _lib.check(status, "paged_decode_attention")
+    if ws is not None:  # the call leaves the per-pair counters (the workspace's first num_seqs x Hkv words) zero
+        assert not torch.any(ws[:num_seqs * kc.shape[2] * 4]).item()
+    return out.view(q.shape), need

@@ -105,9 +105,12 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
     assert decode(num_seqs=0) == _lib.NVHIP_OK
     assert decode() == _lib.NVHIP_EINVAL and "null" in _err()
     ws = lib.nvhip_paged_decode_attention_workspace_size
-    assert ws(32, 1, 16, 8, 128, 256, 8) == 0                 # 256 (sequence, kv head) pairs: no split
+    # 256 pairs: 512 counters (2 KiB) + 2 record blocks per pair of 2 rows x (2 + 128) fp32 in 128-byte lines
+    assert ws(32, 1, 16, 8, 128, 256, 8) == 2048 + 256 * 2 * 288 * 4
     assert ws(1, 1, 16, 8, 128, 256, 64) > 0                  # one long sequence: split over blocks
-    assert ws(1, 1, 16, 8, 128, 256, 64) == 8 * 32 * 2 * (2 + 128) * 4   # 8 pairs x 32 splits of 512 tokens, 2 rows
+    assert ws(1, 1, 16, 8, 128, 256, 64) == 2048 + 8 * 32 * 288 * 4    # 8 pairs x 32 splits of 512 tokens
+    assert ws(520, 1, 16, 8, 128, 256, 8) == 0                # 4160 pairs: one block each
+    assert ws(1, 1, 16, 8, 128, 256, 1) == 0                  # 8 pairs of one 256-token round: nothing to split
     assert ws(0, 1, 16, 8, 128, 256, 8) == 0
 
     pre = lib.nvhip_prefill_attention_bf16

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle
+from helpers import paged_decode_abi
 from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
 
 pytestmark = pytest.mark.gpu
@@ -136,30 +137,49 @@ def test_rejects_bad_arguments():
                                 0.1, True)
 
 
-def _abi_call(q, kc, vc, lens, bt, scale, causal, workspace):
-    """Calls the C entry point directly: workspace None -> one block per (sequence, kv head); else split."""
-    from nanovllm_hip import _lib
-    num_seqs, q_len, Hq, D = q.shape
-    qf = q.reshape(num_seqs * q_len, Hq, D)
-    out = torch.empty_like(qf)
-    lib = _lib.lib()
-    need = lib.nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, kc.shape[2], D, kc.shape[1],
-                                                           bt.shape[1])
-    ws = torch.empty(max(need, 4) // 4 + 1, dtype=torch.float32, device=q.device) if workspace else None
-    status = lib.nvhip_paged_decode_attention_bf16(
-        out.data_ptr(), qf.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), lens.data_ptr(), num_seqs,
-        q_len, Hq, kc.shape[2], D, kc.shape[1], kc.shape[0], bt.shape[1], qf.stride(0), qf.stride(1),
-        out.stride(0), out.stride(1), scale, int(causal), ws.data_ptr() if ws is not None else None,
-        ws.numel() * 4 if ws is not None else 0, _lib.stream_of(q))
-    _lib.check(status, "paged_decode_attention")
-    return out.view(q.shape), need
+def balanced_lens(kind):
+    g = torch.Generator("cpu").manual_seed(len(kind))
+    if kind == "qwen3_b32":      # the decode step's batch: contexts U[512, 2048]
+        return torch.randint(512, 2049, (32,), generator=g).tolist()
+    if kind == "odd_33":         # the median sequence is not paired
+        return torch.randint(1, 3001, (33,), generator=g).tolist()
+    if kind == "equal":          # nothing to cut: every pair whole in its own block
+        return [1000] * 40
+    if kind == "empty_and_long":  # empty and one-token contexts paired with the longest ones
+        return [0, 1, 4000, 3500, 0, 2] + torch.randint(1, 1500, (26,), generator=g).tolist()
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,q_len", [("qwen3_b32", 1), ("odd_33", 1), ("equal", 1), ("empty_and_long", 1),
+                                        ("qwen3_b32", 3)])
+def test_balanced_batches(kind, q_len):
+    """256 .. 512 (sequence, kv head) pairs with a workspace: long and short contexts are paired and the long
+    pair's tail runs in the short pair's block, the two pieces merged inside the kernel by whichever block finishes
+    last. The oracle's values at the bf16 tolerance, the one-block-per-pair path's too, the same bits on a second
+    call, the workspace counters zero after each call (checked in paged_decode_abi)."""
+    lens = balanced_lens(kind)
+    q, kc, vc, lt, bt = make_case(lens, q_len=q_len, seed=len(lens) + q_len, nan_unused=False)
+    ref = oracle.paged_decode_attention(q, kc, vc, lt, bt, 0.1, True)
+    dev = [t.to(DEV) for t in (q, kc, vc, lt, bt)]
+    bal, need = paged_decode_abi(*dev, 0.1, True, workspace=True)
+    again, _ = paged_decode_abi(*dev, 0.1, True, workspace=True)
+    single, _ = paged_decode_abi(*dev, 0.1, True, workspace=False)
+    assert need > 0
+    assert torch.equal(bal, again)
+    for out in (bal, single):
+        torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert torch.all(bal[b] == 0)
+    if kind == "equal":
+        assert torch.equal(bal, single)  # no pair is cut: the same blocks' arithmetic
 
 
 @pytest.mark.parametrize("B,max_len,block_size,seed", [
     (1, 100, 256, 1),      # 8 (sequence, kv head) pairs of at most 4 chunks
     (3, 20000, 256, 2),    # 24 pairs of up to 625 chunks: many splits each
     (20, 300, 16, 3),      # 160 pairs, 16-slot blocks
-    (64, 1200, 256, 4),    # 512 pairs: one block per pair even with a workspace
+    (64, 1200, 256, 4),    # 512 pairs: the pairs of the sequences above the mean context cut in two
     (512, 64, 32, 5),      # 4096 short pairs
 ])
 def test_ragged_batches(B, max_len, block_size, seed):
@@ -172,11 +192,13 @@ def test_ragged_batches(B, max_len, block_size, seed):
     q, kc, vc, lt, bt = make_case(lens, block_size=block_size, seed=seed, nan_unused=False)
     ref = oracle.paged_decode_attention(q, kc, vc, lt, bt, 0.1, True)
     dev = [t.to(DEV) for t in (q, kc, vc, lt, bt)]
-    split, need = _abi_call(*dev, 0.1, True, workspace=True)
-    again, _ = _abi_call(*dev, 0.1, True, workspace=True)
-    single, _ = _abi_call(*dev, 0.1, True, workspace=False)
-    if B * 8 >= 256:
-        assert need == 0                   # enough (sequence, kv head) pairs for the CUs: no split
+    split, need = paged_decode_abi(*dev, 0.1, True, workspace=True)
+    again, _ = paged_decode_abi(*dev, 0.1, True, workspace=True)
+    single, _ = paged_decode_abi(*dev, 0.1, True, workspace=False)
+    if 256 <= B * 8 <= 512:
+        assert need > 0                    # a batch of 256 to 512 pairs: the long pairs cut in two
+    if B * 8 > 512:
+        assert need == 0                   # more pairs: one block each
     if B == 3:
         assert need > 0                    # few pairs over long contexts: split
     assert torch.equal(split, again)
@@ -193,8 +215,8 @@ def test_split_and_single_pass_agree_with_oracle(lens):
     q, kc, vc, lt, bt = make_case(lens, seed=len(lens))
     ref = oracle.paged_decode_attention(q, kc, vc, lt, bt, 0.1, True)
     dev = [t.to(DEV) for t in (q, kc, vc, lt, bt)]
-    split, need = _abi_call(*dev, 0.1, True, workspace=True)
-    single, _ = _abi_call(*dev, 0.1, True, workspace=False)
+    split, need = paged_decode_abi(*dev, 0.1, True, workspace=True)
+    single, _ = paged_decode_abi(*dev, 0.1, True, workspace=False)
     assert need > 0
     for out in (split, single):
         torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=1.6e-2, atol=1e-2)

@@ -1,9 +1,10 @@
-"""nvhip_paged_decode_attention_bf16_noalloc (GPU): the paged decode attention whose context-split records live in
-the library's own device scratch array instead of a caller workspace. Called through the C ABI, it must give
-bitwise the output of nvhip_paged_decode_attention_bf16 with a workspace of the size that entry point asks for (the
-same split policy, the same kernels), on two calls in a row -- the second with a smaller batch and shorter
-contexts, so stale records of the first call would show. (Its refusal of sizes beyond the scratch cannot be
-reached with valid arguments: the split policy never needs more than the 9 MiB the array holds.)"""
+"""nvhip_paged_decode_attention_bf16_noalloc (GPU): the paged decode attention whose pair counters and split records
+live in the library's own device scratch array instead of a caller workspace. Called through the C ABI, it must
+give bitwise the output of nvhip_paged_decode_attention_bf16 with a zero-filled workspace of the size that entry
+point asks for (the same plan, the same kernels), on calls in a row -- a balanced batch of 32 sequences, then
+smaller batches with context splits and shorter contexts, so stale records or counters of a call would show.
+(Its refusal of sizes beyond the scratch cannot be reached with valid arguments: the plan never needs more than
+the 18 MiB the array holds.)"""
 import pytest
 import torch
 
@@ -42,11 +43,11 @@ def call(fn, case, out, extra):
 def test_noalloc_equals_workspace_entry_point_twice():
     lib = _lib.lib()
     fn = noalloc_fn()
-    for seed, batch, max_ctx in ((1, 4, 4096), (2, 2, 1100)):
+    for seed, batch, max_ctx in ((3, 32, 2048), (1, 4, 4096), (2, 2, 1100)):
         case = make_case(seed, batch, max_ctx)
         need = lib.nvhip_paged_decode_attention_workspace_size(batch, 1, HQ, HKV, D, BS, case[5])
         assert need > 0, "the case must split its contexts (the scratch is used)"
-        ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+        ws = torch.zeros(need, dtype=torch.uint8, device=DEV)  # its counters must start at zero
         ref = torch.empty(batch, HQ, D, dtype=torch.bfloat16, device=DEV)
         _lib.check(call(lib.nvhip_paged_decode_attention_bf16, case, ref, [ws.data_ptr(), need]), "workspace call")
         out = torch.full((batch, HQ, D), float("nan"), dtype=torch.bfloat16, device=DEV)
