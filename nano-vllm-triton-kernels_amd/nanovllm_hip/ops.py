@@ -178,16 +178,17 @@ def _matmul_fake(a, b, input_precision):
 # ------------------------------------------------------------------ paged decode attention
 
 # The decode attention's workspaces: the kernel's per-pair counters must be zero before a call and every call leaves
-# them zero, so a workspace is zero-filled once and kept, one per (device, stream) -- calls on one stream never
-# overlap. A workspace is never freed: a captured graph keeps using its address (a larger need adds a new one).
+# them zero, so a workspace is zero-filled once and kept, one per device (a graph captured after an eager warm-up
+# call reuses it, so the zero fill is not captured). Decode attention calls on one device must therefore not run
+# concurrently on unordered streams. A workspace is never freed: a captured graph keeps using its address (a
+# larger need adds a new one).
 _DECODE_WS = {}
 
 
 def _decode_workspace(device, nbytes):
     if nbytes <= 0:
         return None
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    held = _DECODE_WS.setdefault(key, [])
+    held = _DECODE_WS.setdefault(device.index, [])
     if not held or held[-1].numel() < nbytes:
         held.append(torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device))
     return held[-1]
