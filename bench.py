@@ -123,6 +123,7 @@ def bench_lib():
     lib = ctypes.CDLL(path)
     p, i64, i = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     lib.nvhip_bench_stream_copy.argtypes = [p, p, i64, i, p]
+    lib.nvhip_bench_stream_rw.argtypes = [p, p, i64, i, i, p]
     lib.nvhip_bench_qk_pattern.argtypes = [p, p, p, p, i64, i64, i64, p, p, p, i64, p, p, i64, i64, i64, i64, p]
     return lib
 
@@ -132,6 +133,24 @@ def stream_copy(torch, lib, dst, src, nbytes):
     rc = lib.nvhip_bench_stream_copy(dst.data_ptr(), src.data_ptr(), nbytes, 2048,
                                      torch.cuda.current_stream().cuda_stream)
     assert rc == 0, rc
+
+
+def copy_ceiling_us(torch, dev, write_bytes, reads_per_write, steps):
+    """Microseconds per call of a plain nontemporal stream over NSETS rotating buffer pairs that reads
+    reads_per_write x write_bytes and writes write_bytes (nvhip_bench_stream_rw, 8 blocks of 256 threads per CU):
+    the ceiling of an HBM-bound kernel with those byte counts, its launch ramp and drain included."""
+    lib = bench_lib()
+    bufs = [(torch.empty(write_bytes, dtype=torch.uint8, device=dev),
+             torch.empty(write_bytes * reads_per_write, dtype=torch.uint8, device=dev)) for _ in range(NSETS)]
+
+    def fn(i):
+        dst, src = bufs[i % NSETS]
+        rc = lib.nvhip_bench_stream_rw(dst.data_ptr(), src.data_ptr(), write_bytes, reads_per_write, 2048,
+                                       torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, rc
+    ms, _ = time_graph(torch, fn, NSETS, max(40, steps), 20, WARM_S)
+    del bufs
+    return ms * 1e3
 
 
 def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
@@ -309,7 +328,9 @@ def extras(torch, oracle, kernels, dev, steps):
                        NSETS, max(40, steps), 20, WARM_S)
     nbytes = 8192 * (4 * HKV * D * 2 + 4)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    out["store_kvcache_T8192"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    cp = copy_ceiling_us(torch, dev, 8192 * 2 * HKV * D * 2, 1, steps)
+    out["store_kvcache_T8192"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                  "copy_us": round(cp, 3), "frac_of_copy": round(cp / (ms * 1e3), 4)}
     del wl
     T, H, I = 8192, 1024, 3072
     g = torch.Generator("cpu").manual_seed(2)
@@ -317,14 +338,17 @@ def extras(torch, oracle, kernels, dev, steps):
     rs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
     gus = [torch.randn(T, 2 * I, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
     w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
-    for name, fn, nbytes in (
-            ("rms_norm_T8192", lambda i: kernels.rms_norm(xs[i], w, EPS), (2 * T * H + H) * 2),
+    # (name, call, algorithmic bytes, bytes written, reads per byte written) -- the last two size the copy ceiling
+    for name, fn, nbytes, wbytes, rpw in (
+            ("rms_norm_T8192", lambda i: kernels.rms_norm(xs[i], w, EPS), (2 * T * H + H) * 2, T * H * 2, 1),
             ("fused_add_rms_norm_T8192", lambda i: kernels.fused_add_rms_norm(xs[i], rs[i], w, EPS),
-             (4 * T * H + H) * 2),
-            ("silu_and_mul_T8192", lambda i: kernels.silu_and_mul(gus[i]), 3 * T * I * 2)):
+             (4 * T * H + H) * 2, 2 * T * H * 2, 1),
+            ("silu_and_mul_T8192", lambda i: kernels.silu_and_mul(gus[i]), 3 * T * I * 2, T * I * 2, 2)):
         ms, _ = time_graph(torch, fn, NSETS, max(40, steps), 20, WARM_S)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        cp = copy_ceiling_us(torch, dev, wbytes, rpw, steps)
+        out[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                     "copy_us": round(cp, 3), "frac_of_copy": round(cp / (ms * 1e3), 4)}
     del xs, rs, gus
     for layer, (K, N) in GEMM_SHAPES.items():
         M = 2048

@@ -4,6 +4,9 @@
 //  nvhip_bench_stream_copy   dst[i] = src[i] over n 16-byte vectors, grid-stride, nontemporal loads and stores:
 //                            the plain read + write ceiling for a given byte count (and the known-size kernel that
 //                            calibrates rocprof's FETCH_SIZE / WRITE_SIZE counters).
+//  nvhip_bench_stream_rw     dst[i] = src[i] (reads_per_write 1) or src[i] ^ src[n + i] (2: two input streams,
+//                            as SiLU x Mul reads gate and up) over n 16-byte output vectors, grid-stride,
+//                            nontemporal: the ceiling for a kernel's byte counts (read = reads_per_write x write).
 //  nvhip_bench_qk_pattern    the memory traffic of nvhip_qk_norm_rope_kv_bf16 (Qwen3 layout, D = 128, write_k off)
 //                            with the arithmetic taken out: one 256-thread block per token, LANES = 8 lanes per head
 //                            row holding two 16-byte chunks (the halves of RoPE), q rows copied to q_out, k and v rows
@@ -22,6 +25,17 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(u32x4* __restrict__ ds
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
     __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void stream_rw_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
+                                                        int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    u32x4 v = __builtin_nontemporal_load(src + i);
+    if constexpr (R == 2) v ^= __builtin_nontemporal_load(src + n + i);
+    __builtin_nontemporal_store(v, dst + i);
+  }
 }
 
 struct PatternArgs {
@@ -85,6 +99,21 @@ extern "C" int nvhip_bench_stream_copy(void* dst, const void* src, int64_t bytes
   if (!dst || !src || bytes <= 0 || bytes % 16 || blocks <= 0) return -1;
   hipLaunchKernelGGL(stream_copy_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<u32x4*>(dst), static_cast<const u32x4*>(src), bytes / 16);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+extern "C" int nvhip_bench_stream_rw(void* dst, const void* src, int64_t write_bytes, int reads_per_write,
+                                     int blocks, void* stream) {
+  if (!dst || !src || write_bytes <= 0 || write_bytes % 16 || blocks <= 0 ||
+      (reads_per_write != 1 && reads_per_write != 2))
+    return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (reads_per_write == 1)
+    hipLaunchKernelGGL(stream_rw_kernel<1>, dim3(blocks), dim3(256), 0, s, static_cast<u32x4*>(dst),
+                       static_cast<const u32x4*>(src), write_bytes / 16);
+  else
+    hipLaunchKernelGGL(stream_rw_kernel<2>, dim3(blocks), dim3(256), 0, s, static_cast<u32x4*>(dst),
+                       static_cast<const u32x4*>(src), write_bytes / 16);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
