@@ -390,6 +390,9 @@ def extras(torch, oracle, kernels, dev, steps):
                                          "torch_linear_us": round(ms_ref * 1e3, 2)}
         del a, w0, ws
     out["paged_decode_attention_B32"] = decode_attention(torch, dev, steps, g)
+    # a small batch of long contexts: each (sequence, kv head) split over 8 blocks, merged inside the launch
+    out["paged_decode_attention_B4_4k_8k"] = decode_attention(torch, dev, steps, g, batch=4, min_len=4096,
+                                                              max_len=8192)
     out["prefill_attention_4x2048"] = prefill_attention(torch, dev, steps, g)
     out["prefill_chunk256_over_3840"] = prefill_chunk_over_prefix(torch, dev, steps, g)
     n = 4096

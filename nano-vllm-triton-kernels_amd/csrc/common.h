@@ -296,7 +296,7 @@ __device__ __forceinline__ void norm_rope16(const float* x1, const float* x2, fl
 // ---------------------------------------------------------------- device: merging split attention records
 // Element d of row r of one (sequence, kv head) from its context splits' records (fp32 max, sum, two more, O[D] ...
 // at rec0 + s * step for split s, the (max, sum) pair first): O = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),
-// M = max_s m_s, merged in split order; 0 for a row no split saw (M = -inf). Up to 4 splits' loads issue at once.
+// M = max_s m_s, merged in split order; 0 for a row no split saw (M = -inf). Up to 8 splits' loads issue at once.
 // DEVICE_SCOPE: the records were written by other blocks of the running kernel (possibly on other XCDs, whose L2s
 // are not coherent with this one): read with device-scope loads (sc1), which do not return this XCD's L2 copy.
 template <bool DEVICE_SCOPE = false>
@@ -331,14 +331,35 @@ __device__ __forceinline__ float merge_splits(const float* rec0, int64_t step, i
         den = __builtin_fmaf(l[u], f, den);
       }
     }
-  } else {
+  } else {  // groups of 8 splits' loads at once (the max is exact in any order; the sums stay in split order)
+    constexpr int kG = 8;
     float M = -INFINITY;
-    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, ld(rec0 + sp * step));
+    for (int s0 = 0; s0 < splits; s0 += kG) {
+      float m[kG];
+#pragma unroll
+      for (int u = 0; u < kG; ++u) m[u] = s0 + u < splits ? ld(rec0 + (s0 + u) * step) : -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kG; ++u) M = fmaxf(M, m[u]);
+    }
     if (M != -INFINITY) {
-      for (int sp = 0; sp < splits; ++sp) {
-        const float f = exp2f(ld(rec0 + sp * step) - M);
-        num = __builtin_fmaf(ld(rec0 + sp * step + d_off), f, num);
-        den = __builtin_fmaf(ld(rec0 + sp * step + 1), f, den);
+      for (int s0 = 0; s0 < splits; s0 += kG) {
+        float m[kG], l[kG], o[kG];
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+          m[u] = -INFINITY, l[u] = o[u] = 0.0f;
+          if (s0 + u < splits) {
+            m[u] = ld(rec0 + (s0 + u) * step);
+            l[u] = ld(rec0 + (s0 + u) * step + 1);
+            o[u] = ld(rec0 + (s0 + u) * step + d_off);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+          if (s0 + u >= splits) break;
+          const float f = exp2f(m[u] - M);
+          num = __builtin_fmaf(o[u], f, num);
+          den = __builtin_fmaf(l[u], f, den);
+        }
       }
     }
   }
