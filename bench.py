@@ -408,8 +408,9 @@ def extras(torch, oracle, kernels, dev, steps):
 
 
 def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
-    """Paged decode attention of one Qwen3-0.6B layer for a batch of 32 sequences with contexts U[512, 2048]
-    (one query token each), NSETS caches rotated so that the K/V (~170 MB per set) come from HBM.
+    """Paged decode attention of one Qwen3-0.6B layer for `batch` sequences with contexts U[min_len, max_len] (one
+    query token each; the headline decode case: 32 sequences, U[512, 2048]), NSETS caches rotated so that the K/V
+    (~170 MB per set at batch 32) come from HBM.
     bytes = sum(ctx) * Hkv * D * 2 (k, v) * 2 B + q read + out write + context lengths + block-table entries."""
     from nanovllm_hip.kernels.attention import flash_attn_with_kvcache
     lens = torch.randint(min_len, max_len + 1, (batch,), generator=g)
