@@ -141,6 +141,8 @@ def balanced_lens(kind):
     g = torch.Generator("cpu").manual_seed(len(kind))
     if kind == "qwen3_b32":      # the decode step's batch: contexts U[512, 2048]
         return torch.randint(512, 2049, (32,), generator=g).tolist()
+    if kind == "qwen3_b64":
+        return torch.randint(512, 2049, (64,), generator=g).tolist()
     if kind == "odd_33":         # the median sequence is not paired
         return torch.randint(1, 3001, (33,), generator=g).tolist()
     if kind == "equal":          # nothing to cut: every pair whole in its own block
@@ -150,15 +152,22 @@ def balanced_lens(kind):
     raise ValueError(kind)
 
 
-@pytest.mark.parametrize("kind,q_len", [("qwen3_b32", 1), ("odd_33", 1), ("equal", 1), ("empty_and_long", 1),
-                                        ("qwen3_b32", 3)])
-def test_balanced_batches(kind, q_len):
+@pytest.mark.parametrize("kind,q_len,Hq,Hkv,D,bs", [
+    ("qwen3_b32", 1, 16, 8, 128, 256), ("odd_33", 1, 16, 8, 128, 256), ("equal", 1, 16, 8, 128, 256),
+    ("empty_and_long", 1, 16, 8, 128, 256), ("qwen3_b32", 3, 16, 8, 128, 256),
+    ("qwen3_b32", 1, 16, 8, 128, 16),    # 16-slot blocks: chunks and cuts cross cache blocks
+    ("qwen3_b64", 1, 16, 4, 64, 32),     # 4 kv heads (256 pairs), head_dim 64
+    ("qwen3_b32", 1, 32, 16, 128, 256),  # 16 kv heads: 512 pairs
+    ("qwen3_b32", 1, 16, 8, 256, 32),    # head_dim 256: 4-wave blocks, 128-token rounds
+])
+def test_balanced_batches(kind, q_len, Hq, Hkv, D, bs):
     """256 .. 512 (sequence, kv head) pairs with a workspace: long and short contexts are paired and the long
     pair's tail runs in the short pair's block, the two pieces merged inside the kernel by whichever block finishes
     last. The oracle's values at the bf16 tolerance, the one-block-per-pair path's too, the same bits on a second
     call, the workspace counters zero after each call (checked in paged_decode_abi)."""
     lens = balanced_lens(kind)
-    q, kc, vc, lt, bt = make_case(lens, q_len=q_len, seed=len(lens) + q_len, nan_unused=False)
+    q, kc, vc, lt, bt = make_case(lens, q_len=q_len, Hq=Hq, Hkv=Hkv, D=D, block_size=bs, seed=len(lens) + q_len,
+                                  nan_unused=False)
     ref = oracle.paged_decode_attention(q, kc, vc, lt, bt, 0.1, True)
     dev = [t.to(DEV) for t in (q, kc, vc, lt, bt)]
     bal, need = paged_decode_abi(*dev, 0.1, True, workspace=True)
