@@ -39,6 +39,17 @@ int paged_decode_varlen(uint16_t* out, const uint16_t* q, const uint16_t* k_cach
 // independent of the context lengths.
 int64_t paged_decode_varlen_workspace(int64_t num_seqs, int64_t qmax, int64_t Hq, int64_t Hkv, int64_t D);
 
+// The attention workspaces (decode and prefill entry points) start with kAttnCounterBytes of per-(sequence, kv head)
+// counters of the decode attention's in-kernel merge: zero before a call, and every call leaves them zero. Batches
+// of up to kBalanceMaxPairs pairs (and 64 sequences) are balanced by length.
+constexpr int64_t kBalanceMaxPairs = 512, kAttnCounterBytes = kBalanceMaxPairs * 4;
+// Floats per record block of RP rows of the decode attention's split records: whole 128-byte lines when the blocks
+// merge in the kernel (each line is written by one block).
+inline int64_t decode_record_stride(int64_t RP, int64_t D, bool in_kernel) {
+  const int64_t f = RP * (2 + D);
+  return in_kernel ? (f + 31) / 32 * 32 : f;
+}
+
 // Add+RMSNorm (rms_norm.hip) of rows whose x is the sum of `splits` (1..4) fp32 partial products [splits, rows, n]
 // (a split-K GEMM's): x = bf16(partials summed in split order), then exactly nvhip_add_rms_norm_bf16 with a
 // contiguous residual (res_out may alias r). Only for the n add_rms_norm_partials_supported accepts.

@@ -62,6 +62,7 @@ struct DecodeArgs {
   uint32_t* counters;
   int num_seqs;
   int balance;  // pieces from balance_pieces (length-aware) instead of splits x split_len
+  int halves;   // (with counters) block bid takes half bid % 2 of pair bid / 2: its context cut in the middle
 };
 
 // A block's share of one (sequence, kv head) pair: tokens [tok_begin, min(ctx, tok_stop)), split `split` of the
@@ -98,8 +99,9 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 }
 
 
-// Balanced pieces (decode calls of 2 .. 64 sequences with context lengths): the sequences are ranked by context
-// length (longest first, ties by index) and rank r < n / 2 is paired with rank n - 1 - r. For each kv head the long
+// Balanced pieces (calls of at most 64 sequences): the n sequences the kernel takes -- all of a decode call's, the
+// ones with 1 .. q_len queries of a varlen call -- are ranked by context length (longest first, ties by index) and
+// rank r < n / 2 is paired with rank n - 1 - r. For each kv head the long
 // sequence's pair is cut where both blocks get the same work: the long pair's block takes [0, cut), the short
 // pair's block takes [cut, ctx_long) and then its own whole context, so that every block of the launch streams
 // about (ctx_long + ctx_short) / 2 tokens from the start -- instead of the longest pairs streaming alone at the end
@@ -107,9 +109,18 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 // Fills pc with block bid's pieces (the tail first) and returns their count; every wave computes the same plan
 // (one context length per lane).
 __device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piece* pc) {
-  const int lane = threadIdx.x % 64, n = g.num_seqs, cap = g.max_blocks * g.bs;
-  const int c = lane < n ? min(max(g.ctx_lens[lane], 0), cap) : -1;
-  int rank = 0;  // lanes >= n rank after every sequence
+  const int lane = threadIdx.x % 64, cap = g.max_blocks * g.bs;
+  int c = -1;  // this lane's sequence's context length, -1 if the kernel does not take it
+  if (lane < g.num_seqs) {
+    if (g.cu_q != nullptr) {
+      const int lq = g.cu_q[lane + 1] - g.cu_q[lane];
+      if (lq >= 1 && lq <= g.q_len) c = min(max(g.cu_k[lane + 1] - g.cu_k[lane], 0), cap);
+    } else {
+      c = min(max(g.ctx_lens[lane], 0), cap);
+    }
+  }
+  const int n = __popcll(__ballot(c >= 0));
+  int rank = 0;  // the sequences the kernel does not take rank after the others
   for (int j = 0; j < 64; ++j) {
     const int cj = __builtin_amdgcn_readlane(c, j);
     rank += (cj > c || (cj == c && j < lane)) ? 1 : 0;
@@ -479,6 +490,28 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
 // other (a barrier between them: the second piece's chunks reuse the LDS of the first's merge).
 template <int D, int RP, bool ALIGNED, bool FUSE = false>
 __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid, unsigned char* lds) {
+  if (g.halves) {  // the pair's context cut in the middle (whole chunks); a short one stays whole in half 0
+    const int pair = bid / 2, half = bid % 2, b = pair / g.Hkv, cap = g.max_blocks * g.bs;
+    int ctx;
+    if (g.cu_q != nullptr) {
+      const int lq = g.cu_q[b + 1] - g.cu_q[b];
+      if (lq < 1 || lq > g.q_len) return;
+      ctx = min(max(g.cu_k[b + 1] - g.cu_k[b], 0), cap);
+    } else {
+      ctx = min(max(g.ctx_lens[b], 0), cap);
+    }
+    const int cut = min(ctx, ((ctx + 1) / 2 + kChunk - 1) / kChunk * kChunk);
+    if (ctx - cut < kMinTail) {
+      if (half == 0) {
+        Piece pc{pair, 0, 1, 0, INT32_MAX};
+        decode_piece<D, RP, ALIGNED, FUSE>(g, pc, lds);
+      }
+      return;
+    }
+    Piece pc{pair, half, 2, half ? cut : 0, half ? INT32_MAX : cut};
+    decode_piece<D, RP, ALIGNED, FUSE>(g, pc, lds);
+    return;
+  }
   if (g.balance) {
     Piece pc[2];
     const int n = balance_pieces(g, bid, pc);

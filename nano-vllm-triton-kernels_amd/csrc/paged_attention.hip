@@ -85,18 +85,11 @@ __global__ __launch_bounds__(256) void paged_decode_combine(const DecodeArgs g) 
   }
 }
 
-// Floats per record block of RP rows: whole 128-byte lines when the blocks merge in the kernel (each line is
-// written by one block).
-int64_t record_stride(int64_t RP, int64_t D, bool in_kernel) {
-  const int64_t f = RP * (2 + D);
-  return in_kernel ? (f + 31) / 32 * 32 : f;
-}
-
 template <int D, int RP, bool FUSE = false>
 int launch_decode(const DecodeArgs& args, int64_t num_seqs, hipStream_t s) {
   DecodeArgs g = args;
   g.rec_splits = g.balance ? 2 : g.splits;
-  g.rec_stride = record_stride(RP, D, g.counters != nullptr);
+  g.rec_stride = decode_record_stride(RP, D, g.counters != nullptr);
   const int64_t blocks = num_seqs * g.Hkv * g.splits;  // balance: one block per pair (splits = 1)
   const dim3 grid(static_cast<unsigned>(blocks)), block(block_waves(D) * 64);
   if (g.bs % kChunk == 0) hipLaunchKernelGGL((paged_decode_kernel<D, RP, true, FUSE>), grid, block, 0, s, g);
@@ -136,10 +129,8 @@ void split_policy(int64_t num_seqs, int64_t Hkv, int64_t max_ctx, int& splits, i
 // Decode calls with context lengths (not varlen): fewer pairs than CUs -> splits x split_len (split_policy); 256 to
 // 512 pairs of at most 64 sequences -> balance (length-aware: long and short sequences paired, the long pair's
 // tail taken by the short pair's block, balance_pieces);
-// either way the blocks of a split pair merge their records in the kernel. Workspace: 512 uint32 counters, one per
-// pair (zero between calls; a fixed region, so that one workspace can serve calls of any shape), then the record
-// blocks.
-constexpr int64_t kBalanceMaxPairs = 512, kCounterBytes = kBalanceMaxPairs * 4;
+// either way the blocks of a split pair merge their records in the kernel. Workspace: kAttnCounterBytes of counters
+// (zero between calls; a fixed region, so that one workspace can serve calls of any shape), then the record blocks.
 struct DecodePlan {
   int splits = 1, split_len = 0, balance = 0;
   int64_t counter_bytes = 0, bytes = 0;
@@ -156,8 +147,9 @@ DecodePlan decode_plan(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv,
     blocks = pairs * 2;
   }
   if (blocks == 0) return p;
-  p.counter_bytes = kCounterBytes;  // splits x split_len: fewer than 256 pairs; balance: at most 512
-  p.bytes = p.counter_bytes + blocks * record_stride(rows_padded((Hq / Hkv) * q_len), D, true) * int64_t(sizeof(float));
+  p.counter_bytes = kAttnCounterBytes;  // splits x split_len: fewer than 256 pairs; balance: at most 512
+  p.bytes = p.counter_bytes + blocks * decode_record_stride(rows_padded((Hq / Hkv) * q_len), D, true) *
+                                   int64_t(sizeof(float));
   return p;
 }
 int64_t workspace_bytes(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_ctx) {

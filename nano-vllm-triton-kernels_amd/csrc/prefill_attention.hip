@@ -71,6 +71,9 @@ struct PrefillArgs {
   // themselves (one block per (sequence, kv head), dec: its varlen arguments, one split), concurrently with the
   // prefill tiles, instead of a separate launch before this one
   int dec_inline;
+  // dec_extra > 0 (dec.halves): the short sequences' (sequence, kv head) pairs are cut in two; the blocks above
+  // run the first halves, dec_extra blocks appended to the grid (one per pair of the call) the second halves
+  int dec_extra;
   DecodeArgs dec;
 };
 
@@ -105,18 +108,28 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
 
   // Block order. The ids are dealt round-robin over the 8 XCDs (block b runs on XCD b % 8) and each XCD starts its
   // blocks in id order as CUs free up. When the groups (sequence, head group) divide evenly, XCD x takes whole
-  // groups -- all query tiles of a group read the same K/V, which then stays in one XCD's L2 -- and starts them
-  // heaviest query tile (most keys) first across its groups, so that no long tile starts late (longest-first list
-  // scheduling; starting one group's tiles before the next group's left a third of the CUs idle at the end of a
-  // 4 x 2048-token prefill). Otherwise all groups' tiles are dealt heaviest first.
+  // groups -- all query tiles of a group read the same K/V, which then stays in one XCD's L2 -- namely groups x,
+  // x + 8, x + 16, ..., so that every sequence's head groups are spread over the XCDs (contiguous ranges of groups
+  // put a mixed step's prefill chunk, the batch's last sequence, on one XCD), and starts them heaviest query tile
+  // (most keys) first across its groups, so that no long tile starts late (longest-first list scheduling; starting
+  // one group's tiles before the next group's left a third of the CUs idle at the end of a 4 x 2048-token prefill).
+  // Otherwise all groups' tiles are dealt heaviest first.
   // With key splits, the (query tile, split) pairs of a group are its tiles, heaviest (latest query tile, first
   // split) first.
   const int ntile = g.qtiles * g.splits;
-  const int nblk = gridDim.x, ngrp = nblk / ntile;
+  const int nblk = int(gridDim.x) - g.dec_extra, ngrp = nblk / ntile;
+  if (int(blockIdx.x) >= nblk) {  // a second half of a short sequence's pair (the whole block: uniform)
+    if constexpr (PAGED) {
+      const int pair = int(blockIdx.x) - nblk;
+      if (g.dec.bs % 32 == 0) decode_block<D, 16, true>(g.dec, 2 * pair + 1, reinterpret_cast<unsigned char*>(lds));
+      else decode_block<D, 16, false>(g.dec, 2 * pair + 1, reinterpret_cast<unsigned char*>(lds));
+    }
+    return;
+  }
   int grp, ci;
   if (nblk % 8 == 0 && (nblk / 8) % ntile == 0) {
     const int gx = nblk / 8 / ntile, r = blockIdx.x / 8;
-    grp = (blockIdx.x % 8) * gx + r % gx;
+    grp = (r % gx) * 8 + blockIdx.x % 8;
     ci = r / gx;
   } else {
     grp = blockIdx.x % ngrp;
@@ -131,9 +144,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
     // one block per (sequence, kv head) runs the decode attention of the pair (the whole block: b, hg, ci uniform)
     if constexpr (PAGED) {
       if (g.dec_inline && ci == 0 && (hg * HB) % g.G == 0) {
-        const int pair = b * g.Hkv + hg * HB / g.G;
-        if (g.dec.bs % 32 == 0) decode_block<D, 16, true>(g.dec, pair, reinterpret_cast<unsigned char*>(lds));
-        else decode_block<D, 16, false>(g.dec, pair, reinterpret_cast<unsigned char*>(lds));
+        const int pair = b * g.Hkv + hg * HB / g.G, bid = g.dec.halves ? 2 * pair : pair;
+        if (g.dec.bs % 32 == 0) decode_block<D, 16, true>(g.dec, bid, reinterpret_cast<unsigned char*>(lds));
+        else decode_block<D, 16, false>(g.dec, bid, reinterpret_cast<unsigned char*>(lds));
       }
     }
     return;
@@ -495,15 +508,28 @@ int64_t short_queries(int64_t num_seqs, int64_t total_q, int64_t Hq, int64_t Hkv
   return std::min<int64_t>(16 / G, max_seqlen_q);
 }
 
-// Workspace: the prefill kernel's split records, then (16-byte aligned) those of the paged decode kernel's splits.
-int64_t decode_workspace_offset(int64_t prefill_bytes) { return (prefill_bytes + 15) / 16 * 16; }
+// Workspace: kAttnCounterBytes of counters (the decode attention's in-kernel merge: zero before a call, left
+// zero), the prefill kernel's split records, then (16-byte aligned) the short sequences' decode records -- those of
+// the paged decode kernel's splits (no longer sequence in the call), or those of the length-balanced pieces that
+// the prefill kernel's blocks of the short sequences run (a longer sequence in the call).
+int64_t decode_workspace_offset(int64_t prefill_bytes) { return kAttnCounterBytes + (prefill_bytes + 15) / 16 * 16; }
+
+// The short sequences' decode attention inside the prefill launch cuts each (sequence, kv head) pair's context in
+// two (halves) for at most kBalanceMaxPairs pairs (the counters): two record blocks of 16 rows per pair.
+bool inline_halves(int64_t num_seqs, int64_t Hkv) { return num_seqs * Hkv <= kBalanceMaxPairs; }
+int64_t inline_halves_bytes(int64_t num_seqs, int64_t Hkv, int64_t D) {
+  return 2 * num_seqs * Hkv * decode_record_stride(16, D, true) * int64_t(sizeof(float));
+}
 
 int64_t total_workspace_bytes(int64_t num_seqs, int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t Hq, int64_t Hkv,
                               int64_t D, int64_t total_q) {
   const int64_t pre = prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
   const int64_t qs = short_queries(num_seqs, total_q, Hq, Hkv, max_seqlen_q);
-  const int64_t dec = qs > 0 ? paged_decode_varlen_workspace(num_seqs, qs, Hq, Hkv, D) : 0;
-  return dec > 0 ? decode_workspace_offset(pre) + dec : pre;
+  int64_t dec = qs > 0 ? paged_decode_varlen_workspace(num_seqs, qs, Hq, Hkv, D) : 0;
+  if (qs > 0 && max_seqlen_q > qs && inline_halves(num_seqs, Hkv))
+    dec = std::max(dec, inline_halves_bytes(num_seqs, Hkv, D));
+  if (pre == 0 && dec == 0) return 0;
+  return decode_workspace_offset(pre) + dec;
 }
 
 }  // namespace
@@ -583,15 +609,15 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
   g.splits = 1;
   g.split_len = int(std::max<int64_t>(max_seqlen_k, 1));
   const int64_t need = prefill_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, total_q);
-  if (workspace && reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
-    return invalid("prefill_attention: workspace must be 16-byte aligned");
-  if (need > 0 && workspace && workspace_size >= need) {
+  if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return invalid("prefill_attention: workspace must be 256-byte aligned");
+  if (need > 0 && workspace && workspace_size >= kAttnCounterBytes + need) {
     prefill_split_policy(base_blocks, max_seqlen_k, g.splits, g.split_len);
-    g.ws = static_cast<float*>(workspace);
+    g.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kAttnCounterBytes);
   }
   const int64_t blocks = base_blocks * g.splits;
-  if (blocks > INT32_MAX) return invalid("prefill_attention: size too large");
-  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kThreads));
+  if (blocks + num_seqs * Hkv > INT32_MAX) return invalid("prefill_attention: size too large");
+  const dim3 block(static_cast<unsigned>(kThreads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool paged = block_table != nullptr;
   // With the cache (a mixed step, a prefix-cache chunk), sequences with at most 16 / G queries -- the decode
@@ -618,6 +644,17 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
       d.scale_log2 = scale * 1.4426950408889634f, d.causal = causal ? 1 : 0;
       d.splits = 1, d.split_len = int(max_blocks * block_size);
       d.cu_q = cu_seqlens_q, d.cu_k = cu_seqlens_k;
+      // each pair's context cut in two when the workspace holds the counters and the halves' records: the pairs
+      // stream on twice the CUs (the second halves in blocks appended to the grid, which start as the short
+      // sequences' idle query-tile blocks exit -- not in those blocks, which would hold back the long sequence's
+      // last tiles), merged inside the launch
+      if (inline_halves(num_seqs, Hkv) && dws != nullptr &&
+          workspace_size - off >= inline_halves_bytes(num_seqs, Hkv, D)) {
+        d.halves = 1, d.num_seqs = int(num_seqs);
+        d.counters = static_cast<uint32_t*>(workspace), d.ws = dws;
+        d.rec_splits = 2, d.rec_stride = decode_record_stride(16, D, true);
+        g.dec_extra = int(num_seqs * Hkv);
+      }
       g.dec_inline = 1;
     }
     if (!g.dec_inline) {
@@ -629,6 +666,7 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
                                  dws ? workspace_size - off : 0, s);
     }
   }
+  const dim3 grid(static_cast<unsigned>(blocks + g.dec_extra));
 #define NVHIP_PREFILL_LAUNCH(DD, PG, HBV) hipLaunchKernelGGL((prefill_attention_kernel<DD, PG, HBV>), grid, block, 0, s, g)
   if (hb == 2 && D == 64 && paged) NVHIP_PREFILL_LAUNCH(64, true, 2);
   else if (hb == 2 && D == 64) NVHIP_PREFILL_LAUNCH(64, false, 2);

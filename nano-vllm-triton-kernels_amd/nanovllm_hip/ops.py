@@ -177,18 +177,18 @@ def _matmul_fake(a, b, input_precision):
 
 # ------------------------------------------------------------------ paged decode attention
 
-# The decode attention's workspaces: the kernel's per-pair counters must be zero before a call and every call leaves
-# them zero, so a workspace is zero-filled once and kept, one per device (a graph captured after an eager warm-up
-# call reuses it, so the zero fill is not captured). Decode attention calls on one device must therefore not run
-# concurrently on unordered streams. A workspace is never freed: a captured graph keeps using its address (a
-# larger need adds a new one).
-_DECODE_WS = {}
+# The attention workspaces (decode and prefill): they start with the decode attention's per-pair counters, which
+# must be zero before a call and which every call leaves zero, so one workspace is zero-filled once and kept per
+# device, for both ops (a graph captured after an eager warm-up call reuses it, so the zero fill is not captured).
+# Attention calls on one device must therefore not run concurrently on unordered streams. A workspace is never
+# freed: a captured graph keeps using its address (a larger need adds a new one).
+_ATTN_WS = {}
 
 
-def _decode_workspace(device, nbytes):
+def _attn_workspace(device, nbytes):
     if nbytes <= 0:
         return None
-    held = _DECODE_WS.setdefault(device.index, [])
+    held = _ATTN_WS.setdefault(device.index, [])
     if not held or held[-1].numel() < nbytes:
         held.append(torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device))
     return held[-1]
@@ -201,7 +201,7 @@ def _paged_decode_attention_impl(q, k_cache, v_cache, block_table, context_lens,
     out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
     lib = _lib.lib()
     ws_bytes = lib.nvhip_paged_decode_attention_workspace_size(num_seqs, q_len, Hq, Hkv, D, block_size, max_blocks)
-    ws = _decode_workspace(q.device, ws_bytes)
+    ws = _attn_workspace(q.device, ws_bytes)
     status = lib.nvhip_paged_decode_attention_bf16(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
         context_lens.data_ptr(), num_seqs, q_len, Hq, Hkv, D, block_size, num_blocks, max_blocks,
@@ -320,7 +320,7 @@ def _qk_norm_rope_kv_decode_attention_impl(q, k, v, positions, q_w, k_w, eps, co
     out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     lib = _lib.lib()
     ws_bytes = lib.nvhip_paged_decode_attention_workspace_size(B, 1, Hq, Hkv, D, block_size, max_blocks)
-    ws = _decode_workspace(q.device, ws_bytes)
+    ws = _attn_workspace(q.device, ws_bytes)
     cs = cos_sin.reshape(cos_sin.shape[0], -1)
     status = lib.nvhip_qk_norm_rope_kv_decode_attention_bf16(
         out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
@@ -364,7 +364,7 @@ def _prefill_attention_out_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_
     num_seqs = cu_seqlens_q.shape[0] - 1
     lib = _lib.lib()
     ws_bytes = lib.nvhip_prefill_attention_workspace_size(num_seqs, max_seqlen_q, max_seqlen_k, Hq, Hkv, D, Tq)
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    ws = _attn_workspace(q.device, ws_bytes)
     status = lib.nvhip_prefill_attention_bf16(
         out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
         num_seqs, max_seqlen_q, max_seqlen_k, Tq, Hq, Hkv, D, q.stride(0), q.stride(1), k_st, v_st, out.stride(0),

@@ -132,14 +132,16 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
     pws = lib.nvhip_prefill_attention_workspace_size
     rec = (128 + 4) * 4                                       # bytes of one (split, query, head) record
     dec = (2 + 128) * 4 * 16                                  # one short-sequence split record: 16 rows (8 queries x G 2)
+    cnt = 2048                                                # the decode attention's counters, first
     # 4 x 16 query tiles x 8 head pairs fill the CUs: no prefill split, but room for the short-sequence path's
     # splits (4 sequences x 8 kv heads = 32 pairs: at most 8 splits each)
-    assert pws(4, 2048, 2048, 16, 8, 128, 8192) == 4 * 8 * 8 * dec
-    assert pws(17, 240, 2048, 16, 8, 128, 256) == 17 * 8 * 2 * dec  # a mixed step: 136 pairs, at most 2 splits
+    assert pws(4, 2048, 2048, 16, 8, 128, 8192) == cnt + 4 * 8 * 8 * dec
+    # a mixed step: 136 pairs, at most 2 splits -- or the balanced pieces' 2 records per pair
+    assert pws(17, 240, 2048, 16, 8, 128, 256) == cnt + 17 * 8 * 2 * dec
     assert pws(32, 1, 2048, 16, 8, 128, 32) == 0              # 256 pairs: no split anywhere
     assert pws(1, 256, 300, 16, 8, 128, 256) == 0             # keys too few to split
-    assert pws(1, 256, 4096, 16, 8, 128, 256) == 16 * 256 * 16 * rec    # chunk over a prefix: 16 splits of 256
-    assert pws(1, 2048, 2048, 16, 8, 128, 2048) == 2 * 2048 * 16 * rec  # one long prompt: 2 splits of 1024
+    assert pws(1, 256, 4096, 16, 8, 128, 256) == cnt + 16 * 256 * 16 * rec    # chunk over a prefix: 16 splits of 256
+    assert pws(1, 2048, 2048, 16, 8, 128, 2048) == cnt + 2 * 2048 * 16 * rec  # one long prompt: 2 splits of 1024
     assert pws(1, 256, 4096, 16, 8, 256, 256) == 0            # head_dim 256 is not supported
 
     st = lib.nvhip_store_kvcache
