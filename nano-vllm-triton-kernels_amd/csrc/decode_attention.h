@@ -62,7 +62,8 @@ struct DecodeArgs {
   uint32_t* counters;
   int num_seqs;
   int balance;  // pieces from balance_pieces (length-aware) instead of splits x split_len
-  int halves;   // (with counters) block bid takes half bid % 2 of pair bid / 2: its context cut in the middle
+  int halves;   // (with counters; the prefill launch's short sequences) block bid takes half bid % 2 of pair
+                // bid / 2: its context cut in the middle
 };
 
 // A block's share of one (sequence, kv head) pair: tokens [tok_begin, min(ctx, tok_stop)), split `split` of the
@@ -486,45 +487,43 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
   }
 }
 
-// Block bid: split bid % splits of pair bid / splits, or (balance) its one or two balanced pieces, one after the
-// other (a barrier between them: the second piece's chunks reuse the LDS of the first's merge).
-template <int D, int RP, bool ALIGNED, bool FUSE = false>
+// Block bid: split bid % splits of pair bid / splits; or (balance, decode calls) its own pair and then, in a short
+// pair's block, a long pair's tail (a barrier between them: the second piece's chunks reuse the LDS of the first's
+// merge); or (halves, INLINE: the short sequences of the prefill launch) half bid % 2 of pair bid / 2. Each call of
+// the body is a copy of it, so a kernel holds only the modes it runs.
+template <int D, int RP, bool ALIGNED, bool FUSE = false, bool INLINE = false>
 __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid, unsigned char* lds) {
-  if (g.halves) {  // the pair's context cut in the middle (whole chunks); a short one stays whole in half 0
-    const int pair = bid / 2, half = bid % 2, b = pair / g.Hkv, cap = g.max_blocks * g.bs;
-    int ctx;
-    if (g.cu_q != nullptr) {
+  if constexpr (INLINE) {
+    Piece pc{bid, 0, 1, 0, INT32_MAX};
+    if (g.halves) {  // the pair's context cut in the middle (whole chunks); a short one stays whole in half 0
+      const int pair = bid / 2, half = bid % 2, b = pair / g.Hkv, cap = g.max_blocks * g.bs;
       const int lq = g.cu_q[b + 1] - g.cu_q[b];
       if (lq < 1 || lq > g.q_len) return;
-      ctx = min(max(g.cu_k[b + 1] - g.cu_k[b], 0), cap);
-    } else {
-      ctx = min(max(g.ctx_lens[b], 0), cap);
+      const int ctx = min(max(g.cu_k[b + 1] - g.cu_k[b], 0), cap);
+      const int cut = min(ctx, ((ctx + 1) / 2 + kChunk - 1) / kChunk * kChunk);
+      if (ctx - cut < kMinTail) {
+        if (half == 1) return;
+        pc = Piece{pair, 0, 1, 0, INT32_MAX};
+      } else {
+        pc = Piece{pair, half, 2, half ? cut : 0, half ? INT32_MAX : cut};
+      }
     }
-    const int cut = min(ctx, ((ctx + 1) / 2 + kChunk - 1) / kChunk * kChunk);
-    if (ctx - cut < kMinTail) {
-      if (half == 0) {
-        Piece pc{pair, 0, 1, 0, INT32_MAX};
-        decode_piece<D, RP, ALIGNED, FUSE>(g, pc, lds);
+    decode_piece<D, RP, ALIGNED, FUSE>(g, pc, lds);
+  } else {
+    if (g.balance) {
+      Piece pc[2];
+      const int n = balance_pieces(g, bid, pc);
+      decode_piece<D, RP, ALIGNED, FUSE>(g, pc[0], lds);
+      if (n > 1) {
+        __syncthreads();
+        decode_piece<D, RP, ALIGNED, FUSE>(g, pc[1], lds);
       }
       return;
     }
-    Piece pc{pair, half, 2, half ? cut : 0, half ? INT32_MAX : cut};
-    decode_piece<D, RP, ALIGNED, FUSE>(g, pc, lds);
-    return;
+    const int split = bid % g.splits;
+    decode_piece<D, RP, ALIGNED, FUSE>(g, Piece{bid / g.splits, split, g.splits, split * g.split_len,
+                                                split * g.split_len + g.split_len}, lds);
   }
-  if (g.balance) {
-    Piece pc[2];
-    const int n = balance_pieces(g, bid, pc);
-    decode_piece<D, RP, ALIGNED, FUSE>(g, pc[0], lds);
-    if (n > 1) {
-      __syncthreads();
-      decode_piece<D, RP, ALIGNED, FUSE>(g, pc[1], lds);
-    }
-    return;
-  }
-  const int split = bid % g.splits;
-  decode_piece<D, RP, ALIGNED, FUSE>(g, Piece{bid / g.splits, split, g.splits, split * g.split_len,
-                                              split * g.split_len + g.split_len}, lds);
 }
 
 }  // namespace

@@ -121,8 +121,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   if (int(blockIdx.x) >= nblk) {  // a second half of a short sequence's pair (the whole block: uniform)
     if constexpr (PAGED) {
       const int pair = int(blockIdx.x) - nblk;
-      if (g.dec.bs % 32 == 0) decode_block<D, 16, true>(g.dec, 2 * pair + 1, reinterpret_cast<unsigned char*>(lds));
-      else decode_block<D, 16, false>(g.dec, 2 * pair + 1, reinterpret_cast<unsigned char*>(lds));
+      if (g.dec.bs % 32 == 0)
+        decode_block<D, 16, true, false, true>(g.dec, 2 * pair + 1, reinterpret_cast<unsigned char*>(lds));
+      else
+        decode_block<D, 16, false, false, true>(g.dec, 2 * pair + 1, reinterpret_cast<unsigned char*>(lds));
     }
     return;
   }
@@ -145,8 +147,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
     if constexpr (PAGED) {
       if (g.dec_inline && ci == 0 && (hg * HB) % g.G == 0) {
         const int pair = b * g.Hkv + hg * HB / g.G, bid = g.dec.halves ? 2 * pair : pair;
-        if (g.dec.bs % 32 == 0) decode_block<D, 16, true>(g.dec, bid, reinterpret_cast<unsigned char*>(lds));
-        else decode_block<D, 16, false>(g.dec, bid, reinterpret_cast<unsigned char*>(lds));
+        if (g.dec.bs % 32 == 0) decode_block<D, 16, true, false, true>(g.dec, bid, reinterpret_cast<unsigned char*>(lds));
+        else decode_block<D, 16, false, false, true>(g.dec, bid, reinterpret_cast<unsigned char*>(lds));
       }
     }
     return;
