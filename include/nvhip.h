@@ -190,12 +190,15 @@ int nvhip_paged_decode_attention_bf16_noalloc(void* out, const void* q, const vo
  *   step) are computed by the paged decode kernel inside this call.
  *   Query i of a sequence with lq queries sees keys j <= lk - lq + i when causal, all lk otherwise; a query that
  *   sees no key gets zeros. Head h reads kv head h / (Hq / Hkv). D: 64, 128.
- *   workspace: device memory of at least nvhip_prefill_attention_workspace_size(...) bytes, 16-byte aligned
- *   (contents need no initialisation), or NULL / too small: then the keys of a sequence are never split over
- *   blocks. With it, few query tiles over long key ranges (a prompt chunk over its cached prefix) are spread over
- *   the CUs in key ranges whose partial results a second kernel merges, and, with a block table and only short
- *   sequences, their contexts are split as nvhip_paged_decode_attention_bf16 splits them (fewer (sequence, kv
- *   head) pairs than CUs). Calls that share a workspace must be ordered on one stream.
+ *   workspace: device memory of at least nvhip_prefill_attention_workspace_size(...) bytes, 256-byte aligned,
+ *   whose first 2 KiB are ZERO before its first use (the counters of the decode attention's in-kernel merge; every
+ *   call leaves them zero, and the same workspace may serve nvhip_paged_decode_attention_bf16 calls), or NULL /
+ *   too small: then the keys of a sequence are never split over blocks. With it, few query tiles over long key
+ *   ranges (a prompt chunk over its cached prefix) are spread over the CUs in key ranges whose partial results a
+ *   second kernel merges; with a block table and only short sequences, their contexts are split as
+ *   nvhip_paged_decode_attention_bf16 splits them (fewer (sequence, kv head) pairs than CUs); with short sequences
+ *   beside longer ones (a mixed step) each short (sequence, kv head) context is cut in two halves, the second ones
+ *   in blocks appended to the launch, merged inside it. Calls that share a workspace must be ordered on one stream.
  * Numerics: fp32 scores and online softmax, P rounded to bf16 for P.V (as flash-attn), fp32 accumulation, bf16 out.
  */
 int nvhip_prefill_attention_bf16(void* out, const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
