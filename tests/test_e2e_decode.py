@@ -5,7 +5,7 @@ code run eagerly -- the torch-eager path the reference's kernels stand in for).
 With --linear torch both backends run the same projections (torch's F.linear) and differ only in the four kernels
 of the path (RMSNorm, Add+RMSNorm, the fused q/k norm + RoPE + KV write, SiLU x Mul; with the HIP attention also the
 decode step's fused pre-attention + attention launch). Those are bitwise torch-eager on the GPU, so every generated
-token must be identical: the full-size case is the north star's batch-32 decode (28 layers, 32 requests with
+token must be identical: the full-size case is the batch-32 greedy decode of Qwen3-0.6B (28 layers, 32 requests with
 prompts of U[512, 2048] random ids, 32 decode steps: 1056 tokens). With --linear hip the projections run on the HIP
 GEMM, whose fp32 sums are in another order than hipBLASLt's: tokens may then differ where the torch backend's own top two logits
 are within a bf16 step (nano-vllm's tests/test_greedy.py reports cross-backend agreement rather than requiring it
@@ -49,7 +49,7 @@ def test_decode_small(attention, linear, fp32_logits):
 
 
 def test_decode_batch32_full_model_token_identical():
-    """The north star's batch-32 decode at full size: the four kernels only (--linear torch), 32 decode steps after
+    """The batch-32 greedy decode at full size: the four kernels only (--linear torch), 32 decode steps after
     the first token: 32 x 33 tokens, every one identical to the torch-eager backend's."""
     out = run(["--layers", "28", "--batch", "32", "--steps", "32", "--min-len", "512", "--max-len", "2048",
                "--reps", "2", "--linear", "torch"])
