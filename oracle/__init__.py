@@ -2,7 +2,8 @@
 
 A plain-torch fp32 restatement of the reference's eager torch code (the code its Triton kernels replace), run on
 CPU tensors with the same rounding points. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import it, and only as the checker or the timed CPU baseline; the product path (nanovllm_hip) never calls it.
+import it, and only as the reference results are compared with or as the timed CPU baseline; the product path
+(nanovllm_hip) never calls it.
 
 Functions and the reference code each one follows (paths in R3pere/nano-vllm-triton-kernels):
   rms_forward        nanovllm/layers/layernorm.py:20-30   (RMSNorm.rms_forward)
