@@ -160,6 +160,15 @@ __device__ __forceinline__ void store8(uint16_t* p, const u32x4& v) {
   }
 }
 
+// A load from a wave-uniform address through the scalar data cache (s_load): it waits on lgkmcnt instead of
+// queueing behind the wave's vector loads in flight, which retire in issue order. Only for data that no wave of the
+// running kernel writes: the compiler treats it as constant (and may merge or move such loads across stores), and
+// the scalar cache is invalidated when a kernel starts, not by the kernel's own vector stores.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 // 16-byte store (p 16-byte aligned) written through this XCD's L2 at device scope: a buffer store with the sc1
 // cache policy. The L2s of the 8 XCDs are not coherent with each other, so when a kernel ends its dirty L2 lines
 // are written back before the next kernel starts; with plain or nontemporal stores that write-back runs after the

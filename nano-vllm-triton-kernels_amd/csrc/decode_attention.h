@@ -121,11 +121,12 @@ __device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piec
     }
   }
   const int n = __popcll(__ballot(c >= 0));
-  int rank = 0;  // the sequences the kernel does not take rank after the others
-  for (int j = 0; j < 64; ++j) {
-    const int cj = __builtin_amdgcn_readlane(c, j);
-    rank += (cj > c || (cj == c && j < lane)) ? 1 : 0;
-  }
+  // unique keys in that order: (c + 1) above 63 - lane (a context of 2^26 - 1 tokens or more ranks as that), so the
+  // rank is one compare per sequence; the sequences the kernel does not take (key < 64) rank after the others
+  const uint32_t key = (uint32_t(min(c + 1, (1 << 26) - 1)) << 6) | uint32_t(63 - lane);
+  const int ns = min(g.num_seqs, 64);
+  int rank = 0;
+  for (int j = 0; j < ns; ++j) rank += __builtin_amdgcn_readlane(key, j) > key ? 1 : 0;
   const int b = bid / g.Hkv, h = bid % g.Hkv;
   const int rb = __builtin_amdgcn_readlane(rank, b), rp = n - 1 - rb;
   pc[0] = Piece{bid, 0, 1, 0, INT32_MAX};
@@ -177,12 +178,12 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
   const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   int q0 = b * g.q_len, lq = g.q_len, ctx;  // the sequence's first query row, its queries and context length
   if (g.cu_q != nullptr) {
-    q0 = g.cu_q[b];
-    lq = g.cu_q[b + 1] - q0;
-    if (lq < 1 || lq > g.q_len) return;  // the whole block: b is uniform
-    ctx = min(max(g.cu_k[b + 1] - g.cu_k[b], 0), g.max_blocks * g.bs);
+    q0 = load_uniform(g.cu_q + b);  // b is uniform: the sequence's lengths come through the scalar cache
+    lq = load_uniform(g.cu_q + b + 1) - q0;
+    if (lq < 1 || lq > g.q_len) return;  // the whole block
+    ctx = min(max(load_uniform(g.cu_k + b + 1) - load_uniform(g.cu_k + b), 0), g.max_blocks * g.bs);
   } else {
-    ctx = min(max(g.ctx_lens[b], 0), g.max_blocks * g.bs);
+    ctx = min(max(load_uniform(g.ctx_lens + b), 0), g.max_blocks * g.bs);
   }
   const int rows = g.G * lq;
   const int32_t* bt_row = g.bt + int64_t(b) * g.max_blocks;
@@ -206,7 +207,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
   }
   if constexpr (FUSE) {
     static_assert(D == 64 || D == 128, "fused pre-attention: head_dim 64 or 128");
-    const int64_t p = g.positions[b];
+    const int64_t p = load_uniform(g.positions + b);
     const float* cs = g.cos_sin + (p < 0 ? 0 : p >= g.max_pos ? g.max_pos - 1 : p) * g.cs_st;
     // the query rows: lane group q8 / 8 = j0 holds the elements 8 j of the fused norm's lanes j = j0 + 4 u
     // (chunk u of each half), so the sum of squares is rebuilt in that kernel's (torch's) order: per half, lanes
@@ -239,13 +240,13 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
       qf[u + HK] = qrow < rows ? __builtin_bit_cast(bf16x8_t, ob) : bf16x8_t{};
     }
     // the new key (lanes 0 .. D/16-1 of wave 0, the fused norm's own lane layout) and value (the next D/16 lanes)
-    const int32_t slot = g.slots[b];
+    const int32_t slot = load_uniform(g.slots + b);
     const bool writer = ctx > 0 ? (tok_begin <= ctx - 1 && ctx - 1 < tok_stop) : split == 0;
     const bool store = writer && slot >= 0 && slot < g.num_slots;
     // the new rows stand in for what the chunk loads read at position ctx - 1 when that is the slot they go to (a
     // decode step); otherwise (inconsistent slot, clamped context) they are written before any wave reads
-    if (store && ctx > 0 && ctx == g.ctx_lens[b]) {
-      const int t = ctx - 1, blk = bt_row[t / g.bs];
+    if (store && ctx > 0 && ctx == load_uniform(g.ctx_lens + b)) {
+      const int t = ctx - 1, blk = load_uniform(bt_row + t / g.bs);
       fresh_here = blk >= 0 && int64_t(blk) * g.bs + t % g.bs == slot;
     }
     // computed by the wave whose chunk holds the new token (no block barrier), or by wave 0 when they must reach the
@@ -497,9 +498,9 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
     Piece pc{bid, 0, 1, 0, INT32_MAX};
     if (g.halves) {  // the pair's context cut in the middle (whole chunks); a short one stays whole in half 0
       const int pair = bid / 2, half = bid % 2, b = pair / g.Hkv, cap = g.max_blocks * g.bs;
-      const int lq = g.cu_q[b + 1] - g.cu_q[b];
+      const int lq = load_uniform(g.cu_q + b + 1) - load_uniform(g.cu_q + b);
       if (lq < 1 || lq > g.q_len) return;
-      const int ctx = min(max(g.cu_k[b + 1] - g.cu_k[b], 0), cap);
+      const int ctx = min(max(load_uniform(g.cu_k + b + 1) - load_uniform(g.cu_k + b), 0), cap);
       const int cut = min(ctx, ((ctx + 1) / 2 + kChunk - 1) / kChunk * kChunk);
       if (ctx - cut < kMinTail) {
         if (half == 1) return;
