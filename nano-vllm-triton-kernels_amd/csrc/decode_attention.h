@@ -205,14 +205,95 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
 #pragma unroll
     for (int c = 0; c < KC; ++c) qf[c] = bf16x8_t{};
   }
+  const int dg = lane % LPT, ts = lane / LPT;
+  const int tok_end = min(ctx, tok_stop);
+  const int ch_end = (tok_end + kChunk - 1) / kChunk;
+
+  // A chunk's K and V fragments (registers) and which of its tokens are valid. Every load instruction is issued
+  // by all lanes (a lane whose token is not valid reads the first 16 bytes of q) and the loaded values are used as
+  // they are -- invalid tokens are masked out of the scores, so their p is 0 -- so no select waits on a load.
+  struct Tile {
+    bf16x8_t k[PVI], v[PVI];  // row layout: dims 8 (l % LPT) .. +8 of token it * TPI + l / LPT
+    uint64_t kvalid[2];       // bit j: token t0 + 16u + j has a valid block (from lanes j = 0..15)
+  };
+  auto row_of = [&](int t, int64_t base, int t0) -> int64_t {
+    if (t >= ctx) return -1;
+    if constexpr (ALIGNED) return base < 0 ? -1 : base + int64_t(t - t0) * g.Hkv * D;
+    return token_row<D>(g, bt_row, t, kvh);
+  };
+  auto load_tile = [&](Tile& T, int ch, bool scalar_bt) {  // scalar_bt: its block-table entry via s_load
+    const int t0 = ch * kChunk;
+    int64_t base = -1;  // ALIGNED: row offset of token t0; tokens t0 + j follow at + j * Hkv * D
+    if constexpr (ALIGNED) {
+      const int idx = t0 / g.bs - blk0;
+      const int blk = scalar_bt ? load_uniform(bt_row + t0 / g.bs)
+                    : idx < 64 ? __builtin_amdgcn_readlane(bt_lane, idx) : bt_row[t0 / g.bs];
+      base = (blk < 0 || blk >= g.num_blocks) ? -1 : ((int64_t(blk) * g.bs + t0 % g.bs) * g.Hkv + kvh) * D;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) T.kvalid[u] = __ballot(row_of(t0 + 16 * u + lane % 16, base, t0) >= 0);
+#pragma unroll
+    for (int it = 0; it < PVI; ++it) {
+      const int64_t row = row_of(t0 + it * TPI + ts, base, t0);
+      T.k[it] = load_bf16x8_once(row >= 0 ? g.kc + row + 8 * dg : g.q);
+      T.v[it] = load_bf16x8_once(row >= 0 ? g.vc + row + 8 * dg : g.q);
+    }
+  };
+  const int ch0 = tok_begin / kChunk + wave;  // the wave's chunks are ch0, ch0 + NWV, ...
+  Tile A;
+  bool have = false;  // FUSE: A already holds chunk ch0 (requested during the prologue)
   if constexpr (FUSE) {
     static_assert(D == 64 || D == 128, "fused pre-attention: head_dim 64 or 128");
+    constexpr int HK = KC / 2, LN = D / 16;
+    // Every input of the prologue is requested before its first wait (vector loads retire in issue order): the
+    // sequence's position, cache slot and last block-table entry (scalar loads), the query norm weights, in a block
+    // whose range holds the new token that token's key and value rows (lanes 0 .. D/16-1: key, with the key norm
+    // weights; the next D/16 lanes: value), and, once the position is in, the cos / sin rows.
     const int64_t p = load_uniform(g.positions + b);
+    const int32_t slot = load_uniform(g.slots + b);
+    const int blk_last = load_uniform(bt_row + max(ctx - 1, 0) / g.bs);
+    const bool writer = ctx > 0 ? (tok_begin <= ctx - 1 && ctx - 1 < tok_stop) : split == 0;
+    const int e = 8 * (lane % LN);  // this lane's elements of the new row: e .. e+7 and D/2 + e .. +7
+    u32x4 ra = {}, rb = {}, kwa = {}, kwb = {};
+    if (writer && lane < D / 8) {
+      const uint16_t* r = lane < LN ? g.kn + int64_t(b) * g.kn_st + int64_t(kvh) * D
+                                    : g.vn + int64_t(b) * g.vn_st + int64_t(kvh) * D;
+      ra = *reinterpret_cast<const u32x4*>(r + e);
+      rb = *reinterpret_cast<const u32x4*>(r + D / 2 + e);
+      kwa = *reinterpret_cast<const u32x4*>(g.k_w + e);  // used by the key lanes only
+      kwb = *reinterpret_cast<const u32x4*>(g.k_w + D / 2 + e);
+    }
+    u32x4 qwa[HK], qwb[HK];
+#pragma unroll
+    for (int u = 0; u < HK; ++u) {
+      qwa[u] = *reinterpret_cast<const u32x4*>(g.q_w + 32 * u + q8);
+      qwb[u] = *reinterpret_cast<const u32x4*>(g.q_w + D / 2 + 32 * u + q8);
+    }
     const float* cs = g.cos_sin + (p < 0 ? 0 : p >= g.max_pos ? g.max_pos - 1 : p) * g.cs_st;
+    float qcos[HK][8], qsin[HK][8], kcos[8] = {}, ksin[8] = {};
+#pragma unroll
+    for (int u = 0; u < HK; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qcos[u][i] = cs[32 * u + q8 + i], qsin[u][i] = cs[D / 2 + 32 * u + q8 + i];
+    if (writer && lane < LN) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kcos[i] = cs[e + i], ksin[i] = cs[D / 2 + e + i];
+    }
+    // the new key and value rows go to slot `slot`
+    const bool store = writer && slot >= 0 && slot < g.num_slots;
+    // the new rows stand in for what the chunk loads read at position ctx - 1 when that is the slot they go to (a
+    // decode step); otherwise (inconsistent slot, clamped context) they are written before any wave reads
+    if (store && ctx > 0 && ctx == load_uniform(g.ctx_lens + b))
+      fresh_here = blk_last >= 0 && int64_t(blk_last) * g.bs + (ctx - 1) % g.bs == slot;
+    // the wave's first chunk is requested now, its loads in flight during the arithmetic below (its block-table
+    // entry through the scalar cache: no wait on the vector loads); not when the rows must reach the cache first
+    if (!(store && !fresh_here) && ch0 < ch_end) {
+      load_tile(A, ch0, true);
+      have = true;
+    }
     // the query rows: lane group q8 / 8 = j0 holds the elements 8 j of the fused norm's lanes j = j0 + 4 u
     // (chunk u of each half), so the sum of squares is rebuilt in that kernel's (torch's) order: per half, lanes
     // j ^ 1 and j ^ 2 are lane groups 16 and 32 apart and j ^ 4 is the other chunk u; then the two halves
-    constexpr int HK = KC / 2;
     float x1[HK][8], x2[HK][8], p1[HK], p2[HK];
 #pragma unroll
     for (int u = 0; u < HK; ++u) {
@@ -229,47 +310,23 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
     const float rstd = torch_rsqrt(ss * g.inv_d + g.eps);
 #pragma unroll
     for (int u = 0; u < HK; ++u) {
-      const int e = 32 * u + q8;
-      const u32x4 wa = *reinterpret_cast<const u32x4*>(g.q_w + e), wb = *reinterpret_cast<const u32x4*>(g.q_w + D / 2 + e);
-      float c[8], s[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) c[i] = cs[e + i], s[i] = cs[D / 2 + e + i];
       u32x4 oa, ob;
-      norm_rope16(x1[u], x2[u], rstd, wa, wb, c, s, oa, ob);
+      norm_rope16(x1[u], x2[u], rstd, qwa[u], qwb[u], qcos[u], qsin[u], oa, ob);
       qf[u] = qrow < rows ? __builtin_bit_cast(bf16x8_t, oa) : bf16x8_t{};
       qf[u + HK] = qrow < rows ? __builtin_bit_cast(bf16x8_t, ob) : bf16x8_t{};
     }
-    // the new key (lanes 0 .. D/16-1 of wave 0, the fused norm's own lane layout) and value (the next D/16 lanes)
-    const int32_t slot = load_uniform(g.slots + b);
-    const bool writer = ctx > 0 ? (tok_begin <= ctx - 1 && ctx - 1 < tok_stop) : split == 0;
-    const bool store = writer && slot >= 0 && slot < g.num_slots;
-    // the new rows stand in for what the chunk loads read at position ctx - 1 when that is the slot they go to (a
-    // decode step); otherwise (inconsistent slot, clamped context) they are written before any wave reads
-    if (store && ctx > 0 && ctx == load_uniform(g.ctx_lens + b)) {
-      const int t = ctx - 1, blk = load_uniform(bt_row + t / g.bs);
-      fresh_here = blk >= 0 && int64_t(blk) * g.bs + t % g.bs == slot;
-    }
     // computed by the wave whose chunk holds the new token (no block barrier), or by wave 0 when they must reach the
     // cache before any wave reads it
-    constexpr int LN = D / 16;
-    const int e = 8 * (lane % LN);
     const int cw = fresh_here ? ((ctx - 1) / kChunk - tok_begin / kChunk) % NWV : 0;
     if (store && wave == cw && lane < D / 8) {
       if (lane < LN) {
-        const uint16_t* kr = g.kn + int64_t(b) * g.kn_st + int64_t(kvh) * D;
         float k1[8], k2[8];
-        unpack8(*reinterpret_cast<const u32x4*>(kr + e), k1);
-        unpack8(*reinterpret_cast<const u32x4*>(kr + D / 2 + e), k2);
+        unpack8(ra, k1);
+        unpack8(rb, k2);
         const float krstd = torch_rsqrt(torch_row_sumsq<D>(k1, k2) * g.inv_d + g.eps);
-        const u32x4 wa = *reinterpret_cast<const u32x4*>(g.k_w + e), wb = *reinterpret_cast<const u32x4*>(g.k_w + D / 2 + e);
-        float c[8], s[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) c[i] = cs[e + i], s[i] = cs[D / 2 + e + i];
-        norm_rope16(k1, k2, krstd, wa, wb, c, s, na, nb);
+        norm_rope16(k1, k2, krstd, kwa, kwb, kcos, ksin, na, nb);
       } else {
-        const uint16_t* vr = g.vn + int64_t(b) * g.vn_st + int64_t(kvh) * D;
-        na = *reinterpret_cast<const u32x4*>(vr + e);
-        nb = *reinterpret_cast<const u32x4*>(vr + D / 2 + e);
+        na = ra, nb = rb;
       }
       // into the cache for the next steps (with fresh_here this kernel takes them from the registers instead)
       uint16_t* dst = const_cast<uint16_t*>(lane < LN ? g.kc : g.vc) + int64_t(slot) * g.Hkv * D +
@@ -287,42 +344,10 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
   f32x4_t acc[DT];          // O^T dims 16 t + 4 (l / 16) + r of row qrow
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x4_t{0, 0, 0, 0};
-  const int dg = lane % LPT, ts = lane / LPT;
   const int h4 = lane / 16, l16 = lane % 16;
   uint16_t* vs = reinterpret_cast<uint16_t*>(smem) + wave * kChunk * (VPW + KPW);  // this wave's V chunk
   uint16_t* ks = vs + kChunk * VPW;                                                 // and K chunk
-  const int tok_end = min(ctx, tok_stop);
-  const int ch_end = (tok_end + kChunk - 1) / kChunk;
 
-  // A chunk's K and V fragments (registers) and which of its tokens are valid. Every load instruction is issued
-  // by all lanes (a lane whose token is not valid reads the first 16 bytes of q) and the loaded values are used as
-  // they are -- invalid tokens are masked out of the scores, so their p is 0 -- so no select waits on a load.
-  struct Tile {
-    bf16x8_t k[PVI], v[PVI];  // row layout: dims 8 (l % LPT) .. +8 of token it * TPI + l / LPT
-    uint64_t kvalid[2];       // bit j: token t0 + 16u + j has a valid block (from lanes j = 0..15)
-  };
-  auto row_of = [&](int t, int64_t base, int t0) -> int64_t {
-    if (t >= ctx) return -1;
-    if constexpr (ALIGNED) return base < 0 ? -1 : base + int64_t(t - t0) * g.Hkv * D;
-    return token_row<D>(g, bt_row, t, kvh);
-  };
-  auto load_tile = [&](Tile& T, int ch) {
-    const int t0 = ch * kChunk;
-    int64_t base = -1;  // ALIGNED: row offset of token t0; tokens t0 + j follow at + j * Hkv * D
-    if constexpr (ALIGNED) {
-      const int idx = t0 / g.bs - blk0;
-      const int blk = idx < 64 ? __builtin_amdgcn_readlane(bt_lane, idx) : bt_row[t0 / g.bs];
-      base = (blk < 0 || blk >= g.num_blocks) ? -1 : ((int64_t(blk) * g.bs + t0 % g.bs) * g.Hkv + kvh) * D;
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) T.kvalid[u] = __ballot(row_of(t0 + 16 * u + lane % 16, base, t0) >= 0);
-#pragma unroll
-    for (int it = 0; it < PVI; ++it) {
-      const int64_t row = row_of(t0 + it * TPI + ts, base, t0);
-      T.k[it] = load_bf16x8_once(row >= 0 ? g.kc + row + 8 * dg : g.q);
-      T.v[it] = load_bf16x8_once(row >= 0 ? g.vc + row + 8 * dg : g.q);
-    }
-  };
   constexpr float kLazy = 8.0f;
   auto compute_tile = [&](const Tile& T, int ch) {
     const int t0 = ch * kChunk;
@@ -407,9 +432,9 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
 
   // The wave's chunks are first, first + 8, ... (issuing two chunks' loads before computing them, or prefetching
   // the next chunk during the current one, measured no faster).
-  for (int ch = tok_begin / kChunk + wave; ch < ch_end; ch += NWV) {
-    Tile A;
-    load_tile(A, ch);
+  for (int ch = ch0; ch < ch_end; ch += NWV) {
+    if (!have) load_tile(A, ch, false);
+    have = false;
     compute_tile(A, ch);
   }
 
