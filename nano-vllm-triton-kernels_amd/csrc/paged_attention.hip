@@ -352,9 +352,10 @@ extern "C" int nvhip_qk_norm_rope_kv_decode_attention_bf16(
 // GPU the library runs on holds its own copy until the process ends; zero at load, and every call leaves its
 // counters zero). The plan above makes at most 1024 record blocks (fewer than 512 with splits x split_len, 2 per
 // pair of at most 512 pairs when balancing), each of at most 16 rows of (2 + D <= 258) fp32 (16.1 KiB), after at
-// most 2 KiB of counters, so kScratchBytes (18 MiB) covers every size it can choose; a larger need is refused. In host code `scratch` is only a stand-in for the
-// symbol: its device address on the current GPU comes from hipGetSymbolAddress, looked up once per device on the
-// first call made with that device current, and only that address reaches the kernels.
+// most 2 KiB of counters, so kScratchBytes (18 MiB) covers every size it can choose; a larger need is refused. In
+// host code `scratch` is only a stand-in for the symbol: its device address on the current GPU comes from
+// hipGetSymbolAddress, looked up once per device on the first call made with that device current, and only that
+// address reaches the kernels.
 namespace nvhip {
 namespace {
 constexpr int64_t kScratchBytes = int64_t(18) << 20;
