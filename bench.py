@@ -407,7 +407,7 @@ def extras(torch, oracle, kernels, dev, steps):
     return out
 
 
-def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
+def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048, profile=False):
     """Paged decode attention of one Qwen3-0.6B layer for `batch` sequences with contexts U[min_len, max_len] (one
     query token each; the headline decode case: 32 sequences, U[512, 2048]), NSETS caches rotated so that the K/V
     (~170 MB per set at batch 32) come from HBM.
@@ -429,10 +429,24 @@ def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048):
         q = torch.randn(batch, 1, HQ, D, generator=g).to(torch.bfloat16).to(dev)
         sets.append((q, kc, vc, lens.to(torch.int32).to(dev), bt.to(dev)))
     scale = D ** -0.5
-    ms, _ = time_graph(torch, lambda i: flash_attn_with_kvcache(*sets[i % NSETS], scale, True), NSETS,
-                       max(40, steps), 8, WARM_S)
     ctx = int(lens.sum())
     nbytes = ctx * HKV * D * 2 * 2 + 2 * batch * HQ * D * 2 + batch * 4 + sum(need) * 4
+    if profile:  # for rocprofv3 counter runs: `steps` eager launches over the sets, then the calibration copies
+        for i in range(steps):
+            flash_attn_with_kvcache(*sets[i % NSETS], scale, True)
+        torch.cuda.synchronize()
+        lib = bench_lib()
+        n = 256 * 2 ** 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            stream_copy(torch, lib, dst, src, n)
+        torch.cuda.synchronize()
+        print(f"profile: {steps} x paged decode attention (batch {batch}, {ctx} context tokens, {nbytes} algorithmic "
+              f"bytes each); 5 x stream copy of {n} bytes", flush=True)
+        return None
+    ms, _ = time_graph(torch, lambda i: flash_attn_with_kvcache(*sets[i % NSETS], scale, True), NSETS,
+                       max(40, steps), 8, WARM_S)
     gbs = nbytes / (ms * 1e-3) / 1e9
     del sets
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
@@ -638,6 +652,10 @@ def main():
     p.add_argument("--profile-chunk", action="store_true",
                    help="for rocprofv3 kernel traces: --steps eager calls of the prefill attention for a 256-token "
                         "chunk over 3840 cached keys (one Qwen3-0.6B layer)")
+    p.add_argument("--profile-decode", action="store_true",
+                   help="for rocprofv3 counter runs: --steps eager launches of the batch-32 paged decode attention "
+                        "(one Qwen3-0.6B layer, contexts U[512, 2048], the sets rotated), then 5 plain copies of 256 "
+                        "MiB that calibrate the byte counters")
     p.add_argument("--profile-mixed", action="store_true",
                    help="for rocprofv3 kernel traces: build the model, prefill 16 requests, then time the 256-token "
                         "mixed step (16 decodes + a 240-token chunk) --steps times eagerly and --steps times from "
@@ -671,6 +689,9 @@ def main():
         return
     if args.profile_mixed:
         print(json.dumps(e2e_mixed_step(torch, dev, reps=args.steps)), flush=True)
+        return
+    if args.profile_decode:
+        decode_attention(torch, dev, args.steps, torch.Generator("cpu").manual_seed(1234), profile=True)
         return
     if args.profile_e2e:
         print(json.dumps(e2e_decode_step(torch, dev, profile_replays=args.steps)), flush=True)
