@@ -106,10 +106,11 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 // sequence's pair is cut where both blocks get the same work: the long pair's block takes [0, cut), the short
 // pair's block takes [cut, ctx_long) and then its own whole context, so that every block of the launch streams
 // about (ctx_long + ctx_short) / 2 tokens from the start -- instead of the longest pairs streaming alone at the end
-// while the CUs of the short ones idle. Cuts are whole 32-token chunks; a tail under kMinTail tokens is not cut.
+// while the CUs of the short ones idle. Cuts are whole 32-token chunks, moved `shift` tokens towards the long pair's
+// block (the short pair's block runs two pieces); a tail under kMinTail tokens is not cut.
 // Fills pc with block bid's pieces (the tail first) and returns their count; every wave computes the same plan
 // (one context length per lane).
-__device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piece* pc) {
+__device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piece* pc, int shift) {
   const int lane = threadIdx.x % 64, cap = g.max_blocks * g.bs;
   int c = -1;  // this lane's sequence's context length, -1 if the kernel does not take it
   if (lane < g.num_seqs) {
@@ -134,7 +135,7 @@ __device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piec
   const int bp = __ffsll((unsigned long long)__ballot(rank == rp)) - 1;
   const int cb = __builtin_amdgcn_readlane(c, b), cp = __builtin_amdgcn_readlane(c, bp);
   const int c_long = rb < rp ? cb : cp, c_short = rb < rp ? cp : cb;
-  const int cut = min(c_long, (((c_long + c_short + 1) / 2) + kChunk - 1) / kChunk * kChunk);
+  const int cut = min(c_long, max(kChunk, ((c_long + c_short + 1) / 2 + shift + kChunk - 1) / kChunk * kChunk));
   if (c_long - cut < kMinTail) return 1;
   if (rb < rp) {  // the long pair: its head
     pc[0].nsplit = 2, pc[0].tok_stop = cut;
@@ -538,7 +539,12 @@ __device__ __forceinline__ void decode_block(const DecodeArgs& g, const int bid,
   } else {
     if (g.balance) {
       Piece pc[2];
-      const int n = balance_pieces(g, bid, pc);
+      // the cut moves 2 chunks towards the long pair's block: the short pair's block runs a second piece after a
+      // barrier, and in the fused kernel that piece repeats the prologue (query norm + RoPE, the new key / value
+      // row). Decode step (fused kernel) with moves of 0, 1, 2, 3, 4, 6 chunks: 1825, 1814, 1808, 1800, 1803, 1829
+      // us; batch-32 decode attention (plain kernel): 32.8 us up to 2 chunks, 33.6 us at 3. The plain and fused
+      // kernels cut alike, so the fused call stays bitwise the two calls.
+      const int n = balance_pieces(g, bid, pc, 2 * kChunk);
       decode_piece<D, RP, ALIGNED, FUSE>(g, pc[0], lds);
       if (n > 1) {
         __syncthreads();
