@@ -8,9 +8,10 @@ Headline (`value`): the fused q/k RMSNorm + RoPE + paged-KV write at T = 8192 to
                  + n_valid * (2048 k read + 2048 v read + 2048 k cache write + 2048 v cache write) + 512 weights
                = 16 908 * T + 512 with every slot valid (the reference's formula, scripts/bench_qk_rope_kv.py:50-52).
 One step = one launch over the T tokens. NSETS = 8 input/output sets (each with its own block table) rotate from
-launch to launch, 544 MB of qkv in all (twice the 256 MiB Infinity Cache), so the reads come from HBM; exactly
---steps launches are recorded into one HIP graph, warmed up by replaying it (--warmup launches and at least 50 ms),
-and one replay is timed with HIP events on the stream it runs on.
+launch to launch, 544 MB of qkv in all (twice the 256 MiB Infinity Cache), so the reads come from HBM; after
+warm-up launches (--warmup of them and at least 50 ms) and a synchronize, 64 untimed launches are queued and then
+exactly --steps launches are timed with HIP events on the stream they run on (the host submits them while the GPU
+still runs the queued ones, so the timed region holds the launches back to back and no submission gap).
 
 Also reported (under "extra"): the ceilings of the headline on this part -- its own launch shape and memory pattern
 with the arithmetic removed (libnvhip_bench.so's nvhip_bench_qk_pattern) and a plain nontemporal copy of the same
@@ -135,22 +136,98 @@ def stream_copy(torch, lib, dst, src, nbytes):
     assert rc == 0, rc
 
 
-def copy_ceiling_us(torch, dev, write_bytes, reads_per_write, steps):
+def copy_ceiling_us(torch, dev, write_bytes, reads_per_write, steps, windows=1):
     """Microseconds per call of a plain nontemporal stream over NSETS rotating buffer pairs that reads
-    reads_per_write x write_bytes and writes write_bytes (nvhip_bench_stream_rw, 8 blocks of 256 threads per CU):
-    the ceiling of an HBM-bound kernel with those byte counts, its launch ramp and drain included."""
+    reads_per_write x write_bytes and writes write_bytes (nvhip_bench_stream_rw, 8 blocks of 256 threads per CU, or
+    one 16-byte vector per thread for small streams): the ceiling of an HBM-bound kernel with those byte counts, its
+    launch ramp and drain included (the median of `windows` timed windows)."""
     lib = bench_lib()
+    write_bytes = -(-write_bytes // 16) * 16
+    blocks = max(1, min(2048, -(-write_bytes // (16 * 256))))
     bufs = [(torch.empty(write_bytes, dtype=torch.uint8, device=dev),
              torch.empty(write_bytes * reads_per_write, dtype=torch.uint8, device=dev)) for _ in range(NSETS)]
 
     def fn(i):
         dst, src = bufs[i % NSETS]
-        rc = lib.nvhip_bench_stream_rw(dst.data_ptr(), src.data_ptr(), write_bytes, reads_per_write, 2048,
+        rc = lib.nvhip_bench_stream_rw(dst.data_ptr(), src.data_ptr(), write_bytes, reads_per_write, blocks,
                                        torch.cuda.current_stream().cuda_stream)
         assert rc == 0, rc
-    ms, _ = time_graph(torch, fn, NSETS, max(40, steps), 20, WARM_S)
+    ms = sorted(time_graph(torch, fn, NSETS, max(40, steps), 20, WARM_S)[0] for _ in range(windows))[windows // 2]
     del bufs
     return ms * 1e3
+
+
+HBM_SWEEP_POLICIES = {0: "plain", 1: "nontemporal", 2: "plain loads, written-through stores",
+                      3: "nontemporal loads, written-through stores"}
+
+
+def hbm_ceiling(torch, dev, table=False, moved=2 ** 30):
+    """This part's HBM ceiling: the best of a sweep of read-only, write-only and 1:1 copy streams
+    (libnvhip_bench.so's nvhip_bench_hbm_sweep) that move `moved` bytes per launch (default 1 GiB; copy: half read,
+    half written) over rotating buffers of >= 1 GiB in all, four times the 256 MiB Infinity Cache: 1, 2, 4 or 8
+    16-byte vectors in flight per lane; plain, nontemporal or written-through cache policies; grid-stride grids of 1,
+    2, 4, 8 or 16 256-thread blocks per CU or a one-shot grid. Each point is the best of 3 windows of 8 eager
+    launches (4 for 1 GiB) after a 20 ms warm-up of that point. Returns the best point per mode (and every point
+    when table)."""
+    lib = bench_lib()
+    import ctypes
+    lib.nvhip_bench_hbm_sweep.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    moved = moved // 32 * 32
+    nrot = max(1, -(-(2 ** 30) // moved))
+    bufs = [(torch.full((moved,), 1, dtype=torch.uint8, device=dev), torch.full((moved,), 2, dtype=torch.uint8,
+                                                                               device=dev)) for _ in range(nrot)]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream()
+    launches = 4 if nrot == 1 else 8
+    points = []
+    for mode, name in ((0, "read"), (1, "write"), (2, "copy")):
+        nbytes = moved if mode < 2 else moved // 2
+        pols = (0, 1) if mode == 0 else (0, 1, 2) if mode == 1 else (0, 1, 2, 3)
+        for unroll in (1, 2, 4, 8):
+            for pol in pols:
+                for bpc in (1, 2, 4, 8, 16, 0):
+                    blocks = bpc * cus
+                    if mode == 0 and blocks * 256 * 16 > nbytes:
+                        continue
+
+                    def fn(i):
+                        a, b = bufs[i % nrot]
+                        return lib.nvhip_bench_hbm_sweep(b.data_ptr(), None if mode == 1 else a.data_ptr(), nbytes,
+                                                         mode, unroll, pol, blocks, stream.cuda_stream)
+                    t0, i = time.perf_counter(), 0
+                    while time.perf_counter() - t0 < 0.02:
+                        assert fn(i) == 0
+                        i += 1
+                        if i % 64 == 0:
+                            torch.cuda.synchronize()
+                    torch.cuda.synchronize()
+                    best = None
+                    for _ in range(3):
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        for j in range(nrot):  # queued ahead of the start event
+                            assert fn(j) == 0
+                        e0.record(stream)
+                        for j in range(launches):
+                            assert fn(j) == 0
+                        e1.record(stream)
+                        e1.synchronize()
+                        us = e0.elapsed_time(e1) * 1e3 / launches
+                        best = us if best is None else min(best, us)
+                    total = nbytes * (2 if mode == 2 else 1)
+                    points.append({"mode": name, "unroll": unroll, "policy": HBM_SWEEP_POLICIES[pol],
+                                   "blocks_per_cu": bpc or "one-shot", "us": round(best, 2),
+                                   "GB/s": round(total / (best * 1e-6) / 1e9, 1)})
+    del bufs
+    torch.cuda.empty_cache()
+    out = {"bytes_per_launch": moved, "rotating_buffers": nrot, "points": len(points)}
+    for name in ("read", "write", "copy"):
+        top = max((p for p in points if p["mode"] == name), key=lambda p: p["GB/s"])
+        out[name] = {k: v for k, v in top.items() if k != "mode"}
+        out[name]["frac_hbm"] = round(top["GB/s"] / HBM_PEAK_GBS, 4)
+    if table:
+        out["table"] = points
+    return out
 
 
 def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
@@ -187,6 +264,9 @@ def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    # one untimed lead-in replay, then the start event in stream order behind it: the host submits the timed
+    # replay while the GPU still runs the lead-in, so the timed region holds the calls and no idle submission gap
+    graph.replay()
     start.record(stream)
     for _ in range(reps):
         graph.replay()
@@ -195,13 +275,33 @@ def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
     return start.elapsed_time(end) / (reps * n_calls), reps * n_calls
 
 
-def time_steps(torch, fn, steps, warmup, min_warm_s):
-    """Exactly `steps` calls of fn(i) recorded into one HIP graph; the graph is replayed for warm-up (ceil(warmup /
-    steps) replays, and at least min_warm_s of wall time), then one replay -- the `steps` calls and nothing else --
-    is timed with HIP events on the stream it runs on. Returns milliseconds per call."""
-    ms, done = time_graph(torch, fn, steps, steps, warmup, min_warm_s)
-    assert done == steps
-    return ms
+def time_steps(torch, fn, steps, warmup, min_warm_s, lead=64):
+    """Exactly `steps` eager calls fn(0) .. fn(steps - 1), timed with HIP events on the current stream: warm-up calls
+    first (at least `warmup` of them and min_warm_s of wall time: the clock ramp), a synchronize, then `lead`
+    untimed calls queued ahead of the start event, so the GPU runs the timed calls back to back while the host
+    submits them (`lead` calls of ~24 us give the host a 1.5 ms head start). Returns (milliseconds per call, host
+    submission microseconds per timed call). Eager launches: a 20-node graph replay of the same calls measured
+    0.3-0.8 us slower per call than 40- or 200-node replays and than eager calls, whose time matches the kernel
+    trace's mean duration."""
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    i, t0 = 0, time.perf_counter()
+    while i < warmup or time.perf_counter() - t0 < min_warm_s:
+        fn(i)
+        i += 1
+        if i % 256 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    for j in range(lead):
+        fn(j)
+    start.record(stream)
+    h0 = time.perf_counter()
+    for j in range(steps):
+        fn(j)
+    host_us = (time.perf_counter() - h0) * 1e6 / steps
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / steps, host_us
 
 
 def host_cores():
@@ -286,12 +386,12 @@ def ceilings(torch, kernels, wl, steps, head_gbs):
     number of bytes (half read, half written), both over rotating buffers like the headline."""
     lib = bench_lib()
     nbytes = fused_bytes(wl.T, wl.n_valid)
-    ms = time_steps(torch, lambda i: wl.pattern(i, lib, torch), max(40, steps), 20, WARM_S)
+    ms, _ = time_steps(torch, lambda i: wl.pattern(i, lib, torch), max(40, steps), 20, WARM_S)
     pat = nbytes / (ms * 1e-3) / 1e9
     half = nbytes // 2 // 16 * 16
     bufs = [(torch.empty(half, dtype=torch.uint8, device=wl.cos_sin.device),
              torch.empty(half, dtype=torch.uint8, device=wl.cos_sin.device)) for _ in range(NSETS)]
-    ms_c = time_steps(torch, lambda i: stream_copy(torch, lib, bufs[i % NSETS][0], bufs[i % NSETS][1], half),
+    ms_c, _ = time_steps(torch, lambda i: stream_copy(torch, lib, bufs[i % NSETS][0], bufs[i % NSETS][1], half),
                       max(40, steps), 20, WARM_S)
     cp = 2 * half / (ms_c * 1e-3) / 1e9
     del bufs
@@ -316,6 +416,12 @@ def extras(torch, oracle, kernels, dev, steps):
                                WARM_S)[0] for _ in range(windows))[windows // 2]
         out[f"qk_norm_rope_kv_T{T}"] = {"us": round(ms * 1e3, 3),
                                         "GB/s": round(fused_bytes(T, T) / (ms * 1e-3) / 1e9, 1), "sets": nsets}
+        if T == 2048:  # the kernel's memory pattern with the arithmetic removed, over the same rotating sets
+            lib = bench_lib()
+            ms_p, _ = time_graph(torch, lambda i: wl.pattern(i, lib, torch), nsets, max(40, steps), 20, WARM_S)
+            out["qk_pattern_copy_T2048"] = {"us": round(ms_p * 1e3, 3),
+                                            "GB/s": round(fused_bytes(T, T) / (ms_p * 1e-3) / 1e9, 1),
+                                            "fused_frac_of_it": round(ms_p / ms, 4)}
         if T == 2048:  # prefill setting of the reference's README table: k_out written too
             ms, _ = time_graph(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv, True), nsets, max(40, steps),
                                20, WARM_S)
@@ -350,6 +456,34 @@ def extras(torch, oracle, kernels, dev, steps):
         out[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                      "copy_us": round(cp, 3), "frac_of_copy": round(cp / (ms * 1e3), 4)}
     del xs, rs, gus
+    # decode batches (T = 1, 32): launch-latency bound; the median of 5 timed windows, each beside the same-bytes copy
+    for T in (1, 32):
+        xs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+        rs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+        gus = [torch.randn(T, 2 * I, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+        for name, fn, nbytes, wbytes, rpw in (
+                ("rms_norm", lambda i: kernels.rms_norm(xs[i], w, EPS), (2 * T * H + H) * 2, T * H * 2, 1),
+                ("fused_add_rms_norm", lambda i: kernels.fused_add_rms_norm(xs[i], rs[i], w, EPS),
+                 (4 * T * H + H) * 2, 2 * T * H * 2, 1),
+                ("silu_and_mul", lambda i: kernels.silu_and_mul(gus[i]), 3 * T * I * 2, T * I * 2, 2)):
+            ms = sorted(time_graph(torch, fn, NSETS, max(40, steps), 20, WARM_S)[0] for _ in range(5))[2]
+            cp = copy_ceiling_us(torch, dev, wbytes, rpw, steps, windows=5)
+            out[f"{name}_T{T}"] = {"us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                   "copy_us": round(cp, 3), "frac_of_copy": round(cp / (ms * 1e3), 4)}
+        del xs, rs, gus
+    # the per-head q norm of the attention: rows of 128 in a strided [T, 16, 128] view of the qkv output (T = 8192)
+    T = 8192
+    bufs = [torch.randn(T, (HQ + 2 * HKV) * D + PAD, generator=g).to(torch.bfloat16).to(dev) for _ in range(NSETS)]
+    qs = [bb[:, :HQ * D].view(T, HQ, D) for bb in bufs]
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev)
+    ms, _ = time_graph(torch, lambda i: kernels.rms_norm(qs[i], wq, EPS), NSETS, max(40, steps), 20, WARM_S)
+    nbytes = (2 * T * HQ * D + D) * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cp = copy_ceiling_us(torch, dev, T * HQ * D * 2, 1, steps)
+    out["rms_norm_q_heads_T8192"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "rows": T * HQ, "n": D,
+                                     "copy_us": round(cp, 3), "frac_of_copy": round(cp / (ms * 1e3), 4)}
+    del bufs, qs
     for layer, (K, N) in GEMM_SHAPES.items():
         M = 2048
         a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
@@ -665,6 +799,9 @@ def main():
                         "RMSNorm / Add+RMSNorm / SiLU x Mul / store_kvcache at T=8192 and of the fused kernel at "
                         "T=2048 with write_k, then 5 plain copies of 256 MiB (256 MiB read + 256 MiB written each) "
                         "to calibrate the byte counters; prints the launch list instead of the JSON line")
+    p.add_argument("--hbm-sweep", action="store_true",
+                   help="only the HBM ceiling sweep (read-only, write-only and copy streams), every point printed, "
+                        "at 1 GiB per launch and at the headline's bytes per launch")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: only one GPU is measured (the kernel path has no collective: under "
@@ -678,6 +815,11 @@ def main():
     import nanovllm_hip.kernels as kernels
 
     dev = torch.device("cuda:0")
+    if args.hbm_sweep:
+        print(json.dumps(hbm_ceiling(torch, dev, table=True)), flush=True)
+        print(json.dumps(hbm_ceiling(torch, dev, table=True, moved=fused_bytes(args.tokens, args.tokens))),
+              flush=True)
+        return
     if args.profile_gemm:
         profile_gemm(torch, kernels, dev, args.steps, args.gemm_m)
         return
@@ -702,7 +844,7 @@ def main():
         profile_run(torch, oracle, kernels, wl, args.steps)
         return
     # exactly --steps launches (the NSETS sets in turn) recorded into one graph; one replay is timed
-    ms = time_steps(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), args.steps, args.warmup, WARM_S)
+    ms, host_us = time_steps(torch, lambda i: wl.call(i, kernels.qk_norm_rope_kv), args.steps, args.warmup, WARM_S)
     steps_done = args.steps
     nbytes = fused_bytes(T, wl.n_valid)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -717,12 +859,17 @@ def main():
         "config": {"workload": f"qk_norm_rope_kv Qwen3-0.6B attention (Hq 16, Hkv 8, D 128), T={T}, qkv view of "
                                f"[T, 4096+{PAD}], 4 sequences, 512x256-slot paged KV, all slots valid, write_k=False",
                    "tokens": T, "bytes_per_step": nbytes, "rotating_sets": NSETS,
-                   "rotating_read_bytes": NSETS * T * ((HQ + 2 * HKV) * D + PAD) * 2},
+                   "rotating_read_bytes": NSETS * T * ((HQ + 2 * HKV) * D + PAD) * 2,
+                   "timing": f"{steps_done} eager launches timed with HIP events behind 64 queued untimed launches; "
+                             f"host submission {host_us:.1f} us per launch"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
     }
     if not args.no_extra:
         result["extra"] = ceilings(torch, kernels, wl, args.steps, gbs)
+        result["extra"]["hbm_ceiling"] = hbm_ceiling(torch, dev)
+        # the same sweep at the headline's bytes per launch (138.5 MB: the launch ramp and drain at that size)
+        result["extra"]["hbm_ceiling_headline_bytes"] = hbm_ceiling(torch, dev, moved=fused_bytes(T, wl.n_valid))
         result["extra"].update(extras(torch, oracle, kernels, dev, args.steps))
         if not args.no_e2e:
             result["extra"]["e2e_decode_step"] = e2e_decode_step(torch, dev)

@@ -12,12 +12,19 @@
 //                            row holding two 16-byte chunks (the halves of RoPE), q rows copied to q_out, k and v rows
 //                            to their cache slot (skipped for slot -1), the position, slot and cos/sin row read as the
 //                            kernel reads them. What the kernel would take if its math were free.
+//  nvhip_bench_hbm_sweep     one point of a sweep for the part's HBM ceiling: a read-only, write-only or 1:1 copy
+//                            stream over n 16-byte vectors, `unroll` vectors in flight per lane (the loads of an
+//                            iteration issued before its stores), plain / nontemporal / written-through (sc1)
+//                            cache policy, a grid-stride grid of `blocks` 256-thread blocks or (blocks 0) a one-shot
+//                            grid with one iteration per block.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.h"
+
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using nvhip::u32x4;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void stream_copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
@@ -93,7 +100,87 @@ __global__ __launch_bounds__(256) void qk_pattern_kernel(const PatternArgs a) {
   __builtin_nontemporal_store(x2, reinterpret_cast<u32x4*>(dst + HALF + e));
 }
 
+// MODE 0 read only (the loaded words xor-folded; one store per lane only if the fold hits a value random data does
+// not give, so the loads stay live), 1 write only, 2 copy. POL 0 plain loads and stores, 1 nontemporal loads and
+// stores, 2 plain loads and written-through stores, 3 nontemporal loads and written-through stores.
+template <int MODE, int U, int POL>
+__global__ __launch_bounds__(256) void hbm_sweep_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
+                                                        int64_t n, uint32_t salt) {
+  const int64_t step = int64_t(gridDim.x) * 256 * U;
+  u32x4 fold = {0u, 0u, 0u, 0u};
+  for (int64_t base = int64_t(blockIdx.x) * 256 * U + threadIdx.x; base < n; base += step) {
+    u32x4 v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t i = base + int64_t(k) * 256;
+      if constexpr (MODE == 1) {
+        v[k] = u32x4{uint32_t(i), salt, uint32_t(i) ^ salt, uint32_t(k)};
+      } else if (i < n) {
+        v[k] = (POL & 1) ? __builtin_nontemporal_load(src + i) : src[i];
+      } else {
+        v[k] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t i = base + int64_t(k) * 256;
+      if constexpr (MODE == 0) {
+        fold ^= v[k];
+      } else if (i < n) {
+        if constexpr (POL >= 2) nvhip::store16_wt(dst + i, v[k]);
+        else if constexpr (POL == 1) __builtin_nontemporal_store(v[k], dst + i);
+        else dst[i] = v[k];
+      }
+    }
+  }
+  if constexpr (MODE == 0)
+    if (fold[0] == salt && fold[1] == ~salt && fold[2] == salt && fold[3] == ~salt)
+      dst[int64_t(blockIdx.x) * 256 + threadIdx.x] = fold;
+}
+
+template <int MODE, int U>
+void launch_sweep_pol(int pol, dim3 grid, hipStream_t s, u32x4* dst, const u32x4* src, int64_t n) {
+  switch (pol) {
+    case 0: hipLaunchKernelGGL((hbm_sweep_kernel<MODE, U, 0>), grid, dim3(256), 0, s, dst, src, n, 0x9e3779b9u); break;
+    case 1: hipLaunchKernelGGL((hbm_sweep_kernel<MODE, U, 1>), grid, dim3(256), 0, s, dst, src, n, 0x9e3779b9u); break;
+    case 2: hipLaunchKernelGGL((hbm_sweep_kernel<MODE, U, 2>), grid, dim3(256), 0, s, dst, src, n, 0x9e3779b9u); break;
+    default: hipLaunchKernelGGL((hbm_sweep_kernel<MODE, U, 3>), grid, dim3(256), 0, s, dst, src, n, 0x9e3779b9u);
+  }
+}
+
+template <int MODE>
+void launch_sweep_u(int unroll, int pol, dim3 grid, hipStream_t s, u32x4* dst, const u32x4* src, int64_t n) {
+  switch (unroll) {
+    case 1: launch_sweep_pol<MODE, 1>(pol, grid, s, dst, src, n); break;
+    case 2: launch_sweep_pol<MODE, 2>(pol, grid, s, dst, src, n); break;
+    case 4: launch_sweep_pol<MODE, 4>(pol, grid, s, dst, src, n); break;
+    default: launch_sweep_pol<MODE, 8>(pol, grid, s, dst, src, n);
+  }
+}
+
 }  // namespace
+
+// bytes: the stream's length (read-only: bytes read; write-only: bytes written; copy: bytes read = bytes written),
+// a multiple of 16. dst must hold `bytes` (read-only: one 16-byte vector per thread of the grid, written only if
+// the fold hits the salt pattern). blocks 0: one-shot grid of ceil(n / (256 * unroll)) blocks.
+extern "C" int nvhip_bench_hbm_sweep(void* dst, const void* src, int64_t bytes, int mode, int unroll, int policy,
+                                     int blocks, void* stream) {
+  if (!dst || (mode != 1 && !src) || bytes <= 0 || bytes % 16 || mode < 0 || mode > 2 || policy < 0 ||
+      policy > 3 || blocks < 0 || (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8))
+    return -1;
+  const int64_t n = bytes / 16;
+  const int64_t grid = blocks > 0 ? blocks : (n + 256 * unroll - 1) / (256 * unroll);
+  if (grid > INT32_MAX) return -1;
+  if (mode == 0 && grid * 256 > n) return -1;  // the read-only kernel's conditional store lands in dst[0, grid * 256)
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  u32x4* d = static_cast<u32x4*>(dst);
+  const u32x4* r = static_cast<const u32x4*>(src);
+  const dim3 g(static_cast<unsigned>(grid));
+  if (mode == 0) launch_sweep_u<0>(unroll, policy, g, s, d, r, n);
+  else if (mode == 1) launch_sweep_u<1>(unroll, policy, g, s, d, r, n);
+  else launch_sweep_u<2>(unroll, policy, g, s, d, r, n);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
 
 extern "C" int nvhip_bench_stream_copy(void* dst, const void* src, int64_t bytes, int blocks, void* stream) {
   if (!dst || !src || bytes <= 0 || bytes % 16 || blocks <= 0) return -1;

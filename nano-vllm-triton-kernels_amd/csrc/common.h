@@ -45,7 +45,7 @@ int64_t paged_decode_varlen_workspace(int64_t num_seqs, int64_t qmax, int64_t Hq
 constexpr int64_t kBalanceMaxPairs = 512, kAttnCounterBytes = kBalanceMaxPairs * 4;
 // Floats per record block of RP rows of the decode attention's split records: whole 128-byte lines when the blocks
 // merge in the kernel (each line is written by one block).
-inline int64_t decode_record_stride(int64_t RP, int64_t D, bool in_kernel) {
+constexpr int64_t decode_record_stride(int64_t RP, int64_t D, bool in_kernel) {
   const int64_t f = RP * (2 + D);
   return in_kernel ? (f + 31) / 32 * 32 : f;
 }

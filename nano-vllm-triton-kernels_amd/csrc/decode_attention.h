@@ -100,9 +100,10 @@ __device__ __forceinline__ int64_t token_row(const DecodeArgs& g, const int32_t*
 }
 
 
-// Balanced pieces (calls of at most 64 sequences): the n sequences the kernel takes -- all of a decode call's, the
-// ones with 1 .. q_len queries of a varlen call -- are ranked by context length (longest first, ties by index) and
-// rank r < n / 2 is paired with rank n - 1 - r. For each kv head the long
+// Balanced pieces (calls of at most 64 sequences): the n sequences the kernel takes -- a decode call's with a
+// non-empty context, the ones with 1 .. q_len queries and keys of a varlen call -- are ranked by context length
+// (longest first, ties by index) and rank r < n / 2 is paired with rank n - 1 - r. Empty sequences (batch padding)
+// are left out, so padding a batch with them changes no other sequence's pieces. For each kv head the long
 // sequence's pair is cut where both blocks get the same work: the long pair's block takes [0, cut), the short
 // pair's block takes [cut, ctx_long) and then its own whole context, so that every block of the launch streams
 // about (ctx_long + ctx_short) / 2 tokens from the start -- instead of the longest pairs streaming alone at the end
@@ -120,6 +121,7 @@ __device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piec
     } else {
       c = min(max(g.ctx_lens[lane], 0), cap);
     }
+    if (c == 0) c = -1;
   }
   const int n = __popcll(__ballot(c >= 0));
   // unique keys in that order: (c + 1) above 63 - lane (a context of 2^26 - 1 tokens or more ranks as that), so the
@@ -131,6 +133,7 @@ __device__ __forceinline__ int balance_pieces(const DecodeArgs& g, int bid, Piec
   const int b = bid / g.Hkv, h = bid % g.Hkv;
   const int rb = __builtin_amdgcn_readlane(rank, b), rp = n - 1 - rb;
   pc[0] = Piece{bid, 0, 1, 0, INT32_MAX};
+  if (__builtin_amdgcn_readlane(c, b) < 0) return 1;  // a sequence not taken: its own (empty) pair only
   if (rb == rp) return 1;  // the median of an odd batch
   const int bp = __ffsll((unsigned long long)__ballot(rank == rp)) - 1;
   const int cb = __builtin_amdgcn_readlane(c, b), cp = __builtin_amdgcn_readlane(c, bp);

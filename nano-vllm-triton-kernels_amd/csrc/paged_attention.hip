@@ -111,13 +111,23 @@ int launch_decode_rows(const DecodeArgs& g, int64_t num_seqs, int rows, hipStrea
 
 int rows_padded(int64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16; }
 
+// The batch size a plan is chosen for: num_seqs rounded up the way nano-vllm pads a decode batch to the sizes its
+// graphs are recorded for (1, 2, 4, 8, then multiples of 16; model_runner.py:27-29). A batch and the same batch
+// padded with empty sequences (context 0) then get the same plan, and since empty sequences take no part in the
+// length balance (balance_pieces), the real sequences' outputs are bitwise the same either way.
+int64_t plan_batch(int64_t num_seqs) {
+  if (num_seqs <= 2) return num_seqs;
+  if (num_seqs <= 8) return num_seqs <= 4 ? 4 : 8;
+  return (num_seqs + 15) / 16 * 16;
+}
+
 // Context split: only when there are fewer (sequence, kv head) pairs than CUs -- every extra block on a CU pays
 // the start-up latency of its first loads again (measured: 1 -> 2 -> 4 splits of a 32-sequence batch took 42 ->
 // 50 -> 56 us) -- aiming at ~256 blocks in splits of whole 256-token rounds (32 tokens per wave x 8 waves), the
-// longest possible context (max_blocks * block_size) setting the count.
+// longest possible context (max_blocks * block_size) and the padded batch size (plan_batch) setting the count.
 void split_policy(int64_t num_seqs, int64_t Hkv, int64_t max_ctx, int& splits, int& split_len) {
   constexpr int64_t kRound = kChunk * kWaves, kTargetBlocks = 256;
-  const int64_t pairs = std::max<int64_t>(1, num_seqs * Hkv);
+  const int64_t pairs = std::max<int64_t>(1, plan_batch(num_seqs) * Hkv);
   const int64_t want = std::max<int64_t>(1, (kTargetBlocks + pairs - 1) / pairs);
   int64_t len = std::max<int64_t>(kRound, (max_ctx + want - 1) / want);
   len = (len + kRound - 1) / kRound * kRound;
@@ -126,9 +136,10 @@ void split_policy(int64_t num_seqs, int64_t Hkv, int64_t max_ctx, int& splits, i
   split_len = int(std::min<int64_t>(len, INT32_MAX / 2));
 }
 
-// Decode calls with context lengths (not varlen): fewer pairs than CUs -> splits x split_len (split_policy); 256 to
-// 512 pairs of at most 64 sequences -> balance (length-aware: long and short sequences paired, the long pair's
-// tail taken by the short pair's block, balance_pieces);
+// Decode calls with context lengths (not varlen), the pair counts those of the padded batch (plan_batch): fewer
+// pairs than CUs -> splits x split_len (split_policy); 256 to 512 pairs of at most 64 sequences -> balance
+// (length-aware: long and short sequences paired, the long pair's tail taken by the short pair's block,
+// balance_pieces);
 // either way the blocks of a split pair merge their records in the kernel. Workspace: kAttnCounterBytes of counters
 // (zero between calls; a fixed region, so that one workspace can serve calls of any shape), then the record blocks.
 struct DecodePlan {
@@ -138,11 +149,11 @@ struct DecodePlan {
 DecodePlan decode_plan(int64_t num_seqs, int64_t q_len, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_ctx) {
   DecodePlan p;
   split_policy(num_seqs, Hkv, max_ctx, p.splits, p.split_len);
-  const int64_t pairs = num_seqs * Hkv, round = kChunk * block_waves(int(D));
+  const int64_t pairs = num_seqs * Hkv, round = kChunk * block_waves(int(D)), nb = plan_batch(num_seqs);
   int64_t blocks = 0;
   if (p.splits > 1) {
     blocks = pairs * p.splits;
-  } else if (num_seqs >= 2 && num_seqs <= 64 && pairs <= kBalanceMaxPairs && max_ctx >= 2 * round) {
+  } else if (nb >= 2 && nb <= 64 && nb * Hkv <= kBalanceMaxPairs && max_ctx >= 2 * round) {
     p.balance = 1;
     blocks = pairs * 2;
   }
@@ -350,15 +361,19 @@ extern "C" int nvhip_qk_norm_rope_kv_decode_attention_bf16(
 // ------------------------------------------------------------------------------------------------------------
 // Allocation-free variant: the pair counters and split records live in `scratch`, a file-scope device array (each
 // GPU the library runs on holds its own copy until the process ends; zero at load, and every call leaves its
-// counters zero). The plan above makes at most 1024 record blocks (fewer than 512 with splits x split_len, 2 per
-// pair of at most 512 pairs when balancing), each of at most 16 rows of (2 + D <= 258) fp32 (16.1 KiB), after at
-// most 2 KiB of counters, so kScratchBytes (18 MiB) covers every size it can choose; a larger need is refused. In
-// host code `scratch` is only a stand-in for the symbol: its device address on the current GPU comes from
-// hipGetSymbolAddress, looked up once per device on the first call made with that device current, and only that
-// address reaches the kernels.
+// counters zero). The plan above makes at most 2 * kBalanceMaxPairs = 1024 record blocks (2 per pair of at most 512
+// pairs when balancing; fewer than 512 with splits x split_len, which needs fewer than 256 padded pairs and makes
+// at most ceil(256 / padded pairs) splits), each of at most decode_record_stride(16, 256) fp32 (16 rows of
+// 2 + D <= 258 floats, rounded to whole 128-byte lines: 16.1 KiB), after kAttnCounterBytes (2 KiB) of counters:
+// kScratchBytes (16.1 MiB) covers every size it can choose, and a larger need is refused. In host code `scratch` is
+// only a stand-in for the symbol: its device address on the current GPU comes from hipGetSymbolAddress, looked up
+// once per device on the first call made with that device current, and only that address reaches the kernels.
 namespace nvhip {
 namespace {
-constexpr int64_t kScratchBytes = int64_t(18) << 20;
+constexpr int64_t kScratchRecordBlocks = 2 * kBalanceMaxPairs;
+constexpr int64_t kScratchBytes =
+    kAttnCounterBytes + kScratchRecordBlocks * decode_record_stride(16, 256, true) * int64_t(sizeof(float));
+static_assert(kScratchBytes % 256 == 0 && kScratchBytes < (int64_t(17) << 20), "scratch size");
 constexpr int kScratchDevices = 64;
 }  // namespace
 }  // namespace nvhip

@@ -190,6 +190,13 @@ def _attn_workspace(device, nbytes):
         return None
     held = _ATTN_WS.setdefault(device.index, [])
     if not held or held[-1].numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            # a zero fill recorded into the graph would run only at replay, after eager calls that already used the
+            # new workspace's uninitialised counters
+            raise RuntimeError(
+                f"nvhip attention: a {nbytes}-byte workspace is needed inside a graph capture, but the workspace "
+                f"held for this device is {held[-1].numel() if held else 0} bytes; run the same call once eagerly "
+                f"before capturing it")
         held.append(torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device))
     return held[-1]
 

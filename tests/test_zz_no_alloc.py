@@ -2,9 +2,12 @@
 live in the library's own device scratch array instead of a caller workspace. Called through the C ABI, it must
 give bitwise the output of nvhip_paged_decode_attention_bf16 with a zero-filled workspace of the size that entry
 point asks for (the same plan, the same kernels), on calls in a row -- a balanced batch of 32 sequences, then
-smaller batches with context splits and shorter contexts, so stale records or counters of a call would show.
+smaller batches with context splits and shorter contexts, so stale records or counters of a call would show; and
+recorded into a HIP graph after an eager warm-up call (which looks up the scratch address), whose replays, with new
+queries copied into the captured input between them and eager calls of both entry points in between, must each
+give bitwise the workspace entry point's output for those queries.
 (Its refusal of sizes beyond the scratch cannot be reached with valid arguments: the plan never needs more than
-the 18 MiB the array holds.)"""
+the 16.1 MiB the array holds.)"""
 import pytest
 import torch
 
@@ -40,7 +43,7 @@ def call(fn, case, out, extra):
     return fn(*args, *extra, torch.cuda.current_stream().cuda_stream)
 
 
-def test_noalloc_equals_workspace_entry_point_twice():
+def test_noalloc_equals_workspace_entry_point_on_calls_in_a_row():
     lib = _lib.lib()
     fn = noalloc_fn()
     for seed, batch, max_ctx in ((3, 32, 2048), (1, 4, 4096), (2, 2, 1100)):
@@ -54,6 +57,36 @@ def test_noalloc_equals_workspace_entry_point_twice():
         _lib.check(call(fn, case, out, []), "noalloc call")
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"batch {batch}: differs from the workspace entry point"
+
+
+def test_noalloc_graph_replays_equal_workspace_entry_point():
+    lib = _lib.lib()
+    fn = noalloc_fn()
+    case = make_case(5, 32, 2048)  # balanced batch: records merged inside the launch through the scratch counters
+    q, max_blocks = case[0], case[5]
+    need = lib.nvhip_paged_decode_attention_workspace_size(32, 1, HQ, HKV, D, BS, max_blocks)
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    out = torch.empty(32, HQ, D, dtype=torch.bfloat16, device=DEV)
+    _lib.check(call(fn, case, out, []), "eager warm-up")  # scratch address looked up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.check(call(fn, case, out, []), "captured call")
+    g = torch.Generator("cpu").manual_seed(11)
+    other = make_case(6, 4, 4096)  # an eager call of another plan between the replays, through the same scratch
+    other_out = torch.empty(4, HQ, D, dtype=torch.bfloat16, device=DEV)
+    for rep in range(3):
+        q.copy_(torch.randn(32, HQ, D, generator=g).to(torch.bfloat16))
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = torch.empty_like(out)
+        _lib.check(call(lib.nvhip_paged_decode_attention_bf16, case, ref, [ws.data_ptr(), need]), "workspace call")
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}: differs from the workspace entry point"
+        _lib.check(call(fn, other, other_out, []), "eager noalloc call between replays")
+        torch.cuda.synchronize()
 
 
 def test_noalloc_rejects_bad_arguments_before_launching():
