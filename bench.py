@@ -173,7 +173,7 @@ def hbm_ceiling(torch, dev, table=False, moved=2 ** 30):
     import ctypes
     lib.nvhip_bench_hbm_sweep.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    moved = moved // 32 * 32
+    moved = moved // 65536 * 65536  # whole 256-thread x 8-vector iterations of both halves
     nrot = max(1, -(-(2 ** 30) // moved))
     bufs = [(torch.full((moved,), 1, dtype=torch.uint8, device=dev), torch.full((moved,), 2, dtype=torch.uint8,
                                                                                device=dev)) for _ in range(nrot)]

@@ -502,8 +502,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny(const MfmaArgs g) {
 // each wave then reads its fragments from LDS. Read straight from memory, a fragment load touches 16 rows x 64 bytes
 // per wave instruction and streams ~31-36 GB/s per CU from L2; row-contiguous loads of the same bytes 55-75 GB/s.
 // Two LDS stages (round r + 1 stored while round r is multiplied, round r + 2 in flight in registers); row pitch
-// KR + 8 elements. Past K the staged chunks are zero, as gemm_skinny's loads are.
-template <int MT, int NCOL, int NW, int UR, bool SILU = false>
+// KR + 8 elements. Past K the staged chunks are zero, as gemm_skinny's loads are. ONE (K <= KR): the whole K in one
+// round and one stage, every load of the block in flight at once (one memory round trip instead of one per round).
+template <int MT, int NCOL, int NW, int UR, bool SILU = false, bool ONE = false>
 __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
   constexpr int NP = SILU ? 2 : 1;
   constexpr int NT = NCOL >= 16 ? NCOL / 16 : 1;
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
   constexpr int NTH = NW * 64, NCH = (RA + RW) * CPR, CPT = (NCH + NTH - 1) / NTH;
   constexpr int STAGE = (RA + RW) * PITCH;  // bf16 elements
   constexpr int RED = NW * NP * NT * MT * 4 * 64;  // floats of the cross-wave reduction (after the last round)
-  constexpr int LDS_BYTES = 4 * STAGE > 4 * RED ? 4 * STAGE : 4 * RED;
+  constexpr int LDS_BYTES = (ONE ? 2 : 4) * STAGE > 4 * RED ? (ONE ? 2 : 4) * STAGE : 4 * RED;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
   uint16_t* st = reinterpret_cast<uint16_t*>(lds);
@@ -558,10 +559,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
     for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int t = 0; t < MT; ++t) acc[p][j][t] = f32x4_t{};
-  const int rounds = (g.K + KR - 1) / KR;
+  const int rounds = ONE ? 1 : (g.K + KR - 1) / KR;
   load_round(0);
   store_round(0);
-  if (rounds > 1) load_round(1);
+  if (!ONE && rounds > 1) load_round(1);
   __syncthreads();
   for (int r = 0; r < rounds; ++r) {
     const uint16_t* s = st + (r & 1) * STAGE;
@@ -586,7 +587,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
           for (int t = 0; t < MT; ++t)
             acc[p][j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], wf[p][j], acc[p][j][t], 0, 0, 0);
     }
-    if (r + 1 < rounds) {
+    if (!ONE && r + 1 < rounds) {
       store_round((r + 1) & 1);
       if (r + 2 < rounds) load_round(r + 2);
     }
@@ -983,7 +984,21 @@ int launch_skinny_tile(const MfmaArgs& g, hipStream_t s) {
   constexpr int NW = 8;
   const int nout = SILU ? g.N / 2 : g.N;
   const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((g.M + 16 * MT - 1) / (16 * MT))), block(NW * 64);
-  if (NCOL == 8 && MT == 1 && g.K >= 2048) hipLaunchKernelGGL((gemm_skinny_lds<1, 8, NW, 4, SILU>), grid, block, 0, s, g);
+  bool done = false;
+  if constexpr (NCOL == 8 && MT == 1 && !SILU) {
+    if (g.K >= 2048 && g.K <= 13 * 256) {  // the whole K in one round (24 staged rows: LDS <= 160 KB)
+      done = true;
+      switch ((g.K + 255) / 256) {
+#define NVHIP_ONE_ROUND(U) \
+  case U: hipLaunchKernelGGL((gemm_skinny_lds<1, 8, NW, U, false, true>), grid, block, 0, s, g); break;
+        NVHIP_ONE_ROUND(8) NVHIP_ONE_ROUND(9) NVHIP_ONE_ROUND(10) NVHIP_ONE_ROUND(11) NVHIP_ONE_ROUND(12)
+        default: hipLaunchKernelGGL((gemm_skinny_lds<1, 8, NW, 13, false, true>), grid, block, 0, s, g);
+#undef NVHIP_ONE_ROUND
+      }
+    }
+  }
+  if (done) {
+  } else if (NCOL == 8 && MT == 1 && g.K >= 2048) hipLaunchKernelGGL((gemm_skinny_lds<1, 8, NW, 4, SILU>), grid, block, 0, s, g);
   else if (g.N >= 2048 || NCOL == 8) hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 4, SILU>), grid, block, 0, s, g);
   else hipLaunchKernelGGL((gemm_skinny<MT, NCOL, NW, 8, SILU>), grid, block, 0, s, g);
   return check_launch("matmul");
