@@ -9,9 +9,10 @@ Headline (`value`): the fused q/k RMSNorm + RoPE + paged-KV write at T = 8192 to
                = 16 908 * T + 512 with every slot valid (the reference's formula, scripts/bench_qk_rope_kv.py:50-52).
 One step = one launch over the T tokens. NSETS = 8 input/output sets (each with its own block table) rotate from
 launch to launch, 544 MB of qkv in all (twice the 256 MiB Infinity Cache), so the reads come from HBM; after
-warm-up launches (--warmup of them and at least 50 ms) and a synchronize, 64 untimed launches are queued and then
-exactly --steps launches are timed with HIP events on the stream they run on (the host submits them while the GPU
-still runs the queued ones, so the timed region holds the launches back to back and no submission gap).
+warm-up launches (--warmup of them and at least 50 ms) and a synchronize, 64 untimed launches are queued (one
+replay of a HIP graph of them) and then exactly --steps launches are timed with HIP events on the stream they run
+on (the host submits them while the GPU still runs the queued ones, so the timed region holds the launches back to
+back and no submission gap).
 
 Also reported (under "extra"): the ceilings of the headline on this part -- its own launch shape and memory pattern
 with the arithmetic removed (libnvhip_bench.so's nvhip_bench_qk_pattern) and a plain nontemporal copy of the same
@@ -277,12 +278,12 @@ def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
 
 def time_steps(torch, fn, steps, warmup, min_warm_s, lead=64):
     """Exactly `steps` eager calls fn(0) .. fn(steps - 1), timed with HIP events on the current stream: warm-up calls
-    first (at least `warmup` of them and min_warm_s of wall time: the clock ramp), a synchronize, then `lead`
-    untimed calls queued ahead of the start event, so the GPU runs the timed calls back to back while the host
-    submits them (`lead` calls of ~24 us give the host a 1.5 ms head start). Returns (milliseconds per call, host
-    submission microseconds per timed call). Eager launches: a 20-node graph replay of the same calls measured
-    0.3-0.8 us slower per call than 40- or 200-node replays and than eager calls, whose time matches the kernel
-    trace's mean duration."""
+    first (at least `warmup` of them and min_warm_s of wall time: the clock ramp), a synchronize, then one replay of
+    a HIP graph of `lead` calls queued ahead of the start event (one host call: ~1.5 ms of GPU work however slow the
+    host's per-call submission is, e.g. under a profiler), so the GPU runs the timed calls back to back while the host
+    submits them. Returns (milliseconds per call, host submission microseconds per timed call). The timed calls are
+    eager launches: a 20-node graph replay of the same calls measured 0.3-0.8 us slower per call than 40- or 200-node
+    replays and than eager calls, whose time matches the kernel trace's mean duration."""
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     i, t0 = 0, time.perf_counter()
@@ -291,9 +292,15 @@ def time_steps(torch, fn, steps, warmup, min_warm_s, lead=64):
         i += 1
         if i % 256 == 0:
             torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for j in range(lead):
+                fn(j)
     torch.cuda.synchronize()
-    for j in range(lead):
-        fn(j)
+    graph.replay()
     start.record(stream)
     h0 = time.perf_counter()
     for j in range(steps):
@@ -301,6 +308,7 @@ def time_steps(torch, fn, steps, warmup, min_warm_s, lead=64):
     host_us = (time.perf_counter() - h0) * 1e6 / steps
     end.record(stream)
     end.synchronize()
+    del graph
     return start.elapsed_time(end) / steps, host_us
 
 
@@ -860,8 +868,8 @@ def main():
                                f"[T, 4096+{PAD}], 4 sequences, 512x256-slot paged KV, all slots valid, write_k=False",
                    "tokens": T, "bytes_per_step": nbytes, "rotating_sets": NSETS,
                    "rotating_read_bytes": NSETS * T * ((HQ + 2 * HKV) * D + PAD) * 2,
-                   "timing": f"{steps_done} eager launches timed with HIP events behind 64 queued untimed launches; "
-                             f"host submission {host_us:.1f} us per launch"},
+                   "timing": f"{steps_done} eager launches timed with HIP events behind a queued graph of 64 "
+                             f"untimed launches; host submission {host_us:.1f} us per launch"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
     }

@@ -652,7 +652,7 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
   constexpr int R = 16 * MT;                   // rows of this block
   constexpr int NP = SILU ? 2 : 1;
   constexpr int NT = NCOL >= 16 ? NCOL / 16 : 1;
-  static_assert(NCOL == 8 || NCOL == 16, "output columns per block");
+  static_assert(NCOL == 8 || NCOL == 16 || NCOL == 32, "output columns per block");
   static_assert(U >= 1 && U * 32 * NW == K, "one round of k steps");
   __shared__ __attribute__((aligned(16))) uint16_t As[R * KP];
   __shared__ float red[NW][NP][NT][MT][4][64];
@@ -1038,6 +1038,11 @@ int launch_skinny_norm(const NormMfmaArgs& a, hipStream_t s) {
   const int64_t nout = SILU ? a.g.N / 2 : a.g.N, cols16 = (nout + 15) / 16;
   // all rows per block down to 192 column tiles: gate_up + SiLU (3072 outputs) on 192 blocks of 32 rows rather than
   // 384 of 16, which put two blocks on half of the CUs (decode step 1.99 -> 1.97 ms)
+  // qkv (4096 outputs, K = 1024): 32 columns x 16 rows per block (256 blocks), each block's x / residual rows half
+  // of the 32-row tile's: 7.14 -> 6.68 us (sweep of 16 / 32 rows x 8 / 16 / 32 columns; for gate_up + SiLU the
+  // 32 x 16 tile below stays the best)
+  if constexpr (KC == 4 && !SILU)
+    if (a.g.M > 16 && (nout + 31) / 32 * 2 >= 256) return launch_skinny_norm_tile<1, 32, SILU, KC, ADD>(a, s);
   if constexpr (KC == 4)
     if (a.g.M > 16 && cols16 >= 192) return launch_skinny_norm_tile<2, 16, SILU, KC, ADD>(a, s);
   if (cols16 * ((a.g.M + 15) / 16) >= 256) return launch_skinny_norm_tile<1, 16, SILU, KC, ADD>(a, s);
