@@ -160,7 +160,7 @@ int nvhip_paged_decode_attention_bf16(void* out, const void* q, const void* k_ca
 
 /*
  * nvhip_paged_decode_attention_bf16 without a workspace argument and without any allocation: the pair counters and
- * split records go to a device array of this library (18 MiB per GPU, zero at load, held until the process ends;
+ * split records go to a device array of this library (16.1 MiB per GPU, zero at load, held until the process ends;
  * its address on the current device is looked up once per device with hipGetSymbolAddress). No counterpart in the
  * reference: for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same arguments, plan and results as nvhip_paged_decode_attention_bf16 given a
