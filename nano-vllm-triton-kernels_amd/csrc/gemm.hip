@@ -916,6 +916,149 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_f32(const F3
   }
 }
 
+// fp32 MFMA GEMM reading its fragments 16 bytes at a time: both operands sit in LDS as k-contiguous rows (A as it
+// lies; a K-contiguous B as it lies, an N-contiguous B transposed while it is staged), row pitch BK + 4 floats (the
+// 16 rows of a quarter-wave's 16-byte reads fall on distinct banks). The k-tile of 32 is taken in 4 groups of 8 k:
+// lane l (row or column l % 32, half h = l / 32) reads k = 8 g + 4 h .. +4 of group g in one ds_read_b128, and MFMA
+// step s of the group uses its element s -- k = 8 g + s for half 0 and 8 g + 4 + s for half 1 -- so 4 MFMA steps
+// take one read per fragment instead of four. (The products are summed in that k order.) The next group's
+// fragments are read while the current group's MFMAs issue; the next k-tile is loaded into registers at the start
+// of a k-tile and stored into the other LDS stage after its second group.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool B_NMAJOR, bool TF32, bool PF = true>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_f32q(const F32Args g) {
+  constexpr int NT = 64 * WAVES_M * WAVES_N, BK = 32, P = BK + 4;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
+  constexpr int CHA = BM * BK / 4 / NT, CHB = BN * BK / 4 / NT;  // 16-byte chunks per thread per k-tile
+  static_assert(FM >= 1 && FN >= 1 && CHA >= 1 && CHB >= 1 && CHA * NT * 4 == BM * BK && CHB * NT * 4 == BN * BK,
+                "tile shape");
+  static_assert(!B_NMAJOR || (BN % 32 == 0 && BK % 8 == 0), "N-contiguous B staging");
+  __shared__ __attribute__((aligned(16))) float lds[2][(BM + BN) * P];  // [stage][A rows | B rows]
+  int pid_m, pid_n;
+  tile_coords(blockIdx.x, g.M, g.N, BM, BN, pid_m, pid_n);
+  const int m0 = pid_m * BM, n0 = pid_n * BN;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+  // A (and a K-contiguous B) chunk c: row c / 8, k 4 (c % 8) .. +4. N-contiguous B chunk c: k row kk, columns
+  // 4 nn .. +4 with 8 lanes along n (128 contiguous bytes) and 8 along k
+  const float* asrc[CHA];
+  const float* bsrc[CHB];
+  int adst[CHA], akc[CHA], bdst[CHB], bkc[CHB];
+#pragma unroll
+  for (int i = 0; i < CHA; ++i) {
+    const int c = tid + NT * i, row = c / 8;
+    akc[i] = 4 * (c % 8);
+    asrc[i] = g.a + int64_t(min(m0 + row, g.M - 1)) * g.sam + akc[i];
+    adst[i] = row * P + akc[i];
+  }
+#pragma unroll
+  for (int i = 0; i < CHB; ++i) {
+    const int c = tid + NT * i;
+    if constexpr (B_NMAJOR) {
+      constexpr int NH = BN / 32;  // groups of 8 column chunks
+      const int nn = ((c / 64) % NH) * 8 + c % 8, kk = (c / (64 * NH)) * 8 + (c / 8) % 8;
+      bkc[i] = kk;
+      bsrc[i] = g.b + min(n0 + 4 * nn, g.N - 4);
+      bdst[i] = BM * P + 4 * nn * P + kk;
+    } else {
+      const int row = c / 8;
+      bkc[i] = 4 * (c % 8);
+      bsrc[i] = g.b + int64_t(min(n0 + row, g.N - 1)) * g.sbn + bkc[i];
+      bdst[i] = BM * P + row * P + bkc[i];
+    }
+  }
+  f32x4_t ra[CHA], rb[CHB];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CHA; ++i)
+      ra[i] = (k0 + akc[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(asrc[i] + k0) : f32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < CHB; ++i) {
+      if constexpr (B_NMAJOR)
+        rb[i] = (k0 + bkc[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(bsrc[i] + int64_t(k0 + bkc[i]) * g.sbk)
+                                    : f32x4_t{0, 0, 0, 0};
+      else
+        rb[i] = (k0 + bkc[i] < g.K) ? *reinterpret_cast<const f32x4_t*>(bsrc[i] + k0) : f32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto tf = [](float x) { return TF32 ? round_tf32(x) : x; };
+  auto lstore = [&](int st) {
+    float* l = lds[st];
+#pragma unroll
+    for (int i = 0; i < CHA; ++i)
+      *reinterpret_cast<f32x4_t*>(l + adst[i]) = f32x4_t{tf(ra[i][0]), tf(ra[i][1]), tf(ra[i][2]), tf(ra[i][3])};
+#pragma unroll
+    for (int i = 0; i < CHB; ++i) {
+      if constexpr (B_NMAJOR) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) l[bdst[i] + e * P] = tf(rb[i][e]);
+      } else {
+        *reinterpret_cast<f32x4_t*>(l + bdst[i]) = f32x4_t{tf(rb[i][0]), tf(rb[i][1]), tf(rb[i][2]), tf(rb[i][3])};
+      }
+    }
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16_t{};
+  const int fr = lane % 32, fh = lane / 32;
+  const int nk = (g.K + BK - 1) / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) gload((kt + 1) * BK);
+    const float* la = lds[kt & 1];
+    const float* lb = lds[kt & 1] + BM * P;
+    f32x4_t af[2][FM], bf[2][FN];  // fragments of group q and q + 1
+    auto frags = [&](int q, int sl) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[sl][i] = *reinterpret_cast<const f32x4_t*>(la + (wm * WM + i * 32 + fr) * P + 8 * q + 4 * fh);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[sl][j] = *reinterpret_cast<const f32x4_t*>(lb + (wn * WN + j * 32 + fr) * P + 8 * q + 4 * fh);
+    };
+    if (PF) frags(0, 0);
+#pragma unroll
+    for (int q = 0; q < BK / 8; ++q) {
+      if (PF && q + 1 < BK / 8) frags(q + 1, (q + 1) & 1);
+      if (!PF) frags(q, q & 1);
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[q & 1][j][st], af[q & 1][i][st], acc[i][j], 0, 0, 0);
+      if (q == 1 && more) lstore((kt + 1) & 1);  // the other stage: nobody reads it during this k-tile
+    }
+    __syncthreads();
+  }
+  // lane holds C row m0 + wm*WM + i*32 + lane%32, columns n0 + wn*WN + j*32 + 8*q + 4*(lane/32) .. +4
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WM + i * 32 + fr;
+    if (m >= g.M) continue;
+    float* crow = g.c + int64_t(m) * g.scm;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * WN + j * 32 + 8 * q + 4 * fh;
+        const f32x4_t v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        if (n + 4 <= g.N && (reinterpret_cast<uintptr_t>(crow + n) & 15) == 0) {
+          *reinterpret_cast<f32x4_t*>(crow + n) = v;
+        } else {
+          for (int e = 0; e < 4 && n + e < g.N; ++e) crow[n + e] = v[e];
+        }
+      }
+  }
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int RS, bool KTAIL, bool SILU, bool BNM = false>
 int launch_mfma(const MfmaArgs& g, hipStream_t s) {
   const int64_t tiles = int64_t((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
@@ -1059,15 +1202,17 @@ int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   return launch_mfma_shape<1, false, SILU>(g, s);
 }
 
-// 256x256 tiles (16 waves) when they fill the CUs at least once, else 128x128 (8 waves). The 256x256 kernel with
-// tf32 rounding of an N-major B needs more than the 128 VGPRs a 1024-thread block leaves a lane: 128x128 there.
+// 256x256 tiles (16 waves, 16-byte fragment reads) when they fill the CUs at least once, else 128x128 (8 waves).
+// 4096^3 "ieee" with an N-contiguous B: 1051 us with gemm_mfma_f32<256, 256, 4, 4> -> 982 us (torch.matmul 914 us);
+// 128x128 / 256x256 tiles with 4 or 8 waves of 64x64 .. 128x128 measured 1042-1108 us. The tf32 rounding adds
+// registers that the next group's fragments would spill, so that variant reads them as it goes.
 template <bool B_NMAJOR, bool TF32>
 int launch_f32(const F32Args& g, hipStream_t s) {
   const int64_t big = int64_t((g.M + 255) / 256) * ((g.N + 255) / 256);
-  if (big >= 256 && !(B_NMAJOR && TF32)) {
+  if (big >= 256) {
     if (big > INT32_MAX) return invalid("matmul: matrix too large");
-    if constexpr (!(B_NMAJOR && TF32))
-      hipLaunchKernelGGL((gemm_mfma_f32<256, 256, 4, 4, B_NMAJOR, TF32>), dim3(unsigned(big)), dim3(1024), 0, s, g);
+    hipLaunchKernelGGL((gemm_mfma_f32q<256, 256, 4, 4, B_NMAJOR, TF32, !TF32>), dim3(unsigned(big)), dim3(1024), 0, s,
+                       g);
     return check_launch("matmul");
   }
   const int64_t tiles = int64_t((g.M + 127) / 128) * ((g.N + 127) / 128);
