@@ -157,6 +157,25 @@ def test_fp32_4096_cube():
     torch.testing.assert_close(c.double(), ref, rtol=1e-4, atol=1e-4 * 64)
 
 
+@pytest.mark.parametrize("M,N,K,b_transposed,prec", [
+    (4096, 4096, 2048, False, "tf32"), (4096, 4096, 2048, True, "ieee"), (4096, 4096, 2048, True, "tf32"),
+    (4000, 4100, 1000, False, "ieee"), (4000, 4100, 1000, True, "tf32"),  # partial tiles, K not a multiple of 32
+])
+def test_fp32_large_tiles(M, N, K, b_transposed, prec):
+    """Products with at least 256 tiles of 256 x 256 take the 16-wave kernel with 16-byte fragment reads (k
+    permuted within groups of 8): both B layouts, both precisions, ragged edges and a K tail, against float64 on the
+    GPU at the reference's tolerances."""
+    g = torch.Generator("cpu").manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).to(DEV)
+    b = torch.randn(N, K, generator=g).to(DEV).t() if b_transposed else torch.randn(K, N, generator=g).to(DEV)
+    c = matmul(a, b, prec)
+    ref = a.double() @ b.double()
+    rtol, atol = TOL[("fp32", prec)]
+    torch.testing.assert_close(c.double(), ref, rtol=rtol, atol=atol * math.sqrt(K))
+    if prec == "ieee":  # and not silently tf32: a tf32 product of the same inputs is off by far more
+        assert (c.double() - ref).abs().max().item() < 1e-2 < (matmul(a, b, "tf32").double() - ref).abs().max().item()
+
+
 def test_strided_views_and_empty():
     g = torch.Generator("cpu").manual_seed(5)
     big_a = torch.randn(70, 300, generator=g).to(torch.bfloat16).to(DEV)
