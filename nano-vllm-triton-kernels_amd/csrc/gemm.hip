@@ -625,6 +625,85 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------------------
+// Wide decode outputs with K = 1024 (the tied LM head: 32 x 151 936 x 1024, a 311 MB weight): the block stages its
+// A rows (all M <= 32 of them, the whole K) in LDS once, and wave gw of the grid's nw takes the 16-column W tiles
+// gw, gw + nw, ... (neighbouring waves read neighbouring tiles): W fragments (16 bytes per lane per 32-wide k step)
+// loaded straight from memory, the second half of a tile and the first half of the next one in flight while a
+// half is multiplied, A fragments read from LDS four k steps at a time, v_mfma_f32_16x16x32_bf16 with the 32 k
+// steps of a tile accumulated in k order (no cross-wave sum). 151 936 x 1024 at M = 32, the weight from HBM:
+// 63.3 us against 67.1 us for the 64-column LDS-staged blocks (gemm_skinny_lds); with each wave taking a
+// contiguous range of tiles instead 67.6 us, with nontemporal W loads 71.0 us, with the A fragments kept in
+// registers (one wave per SIMD, 256 blocks of 4 waves) 73.2 us.
+template <int MT>
+__global__ __launch_bounds__(512) void gemm_wide_k1024(const MfmaArgs g) {
+  constexpr int KS = 32, HS = KS / 2, K = 1024, P = K + 8;  // row pitch: 16 rows of a fragment read on distinct banks
+  __shared__ __attribute__((aligned(16))) uint16_t As[16 * MT * P];
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  for (int c = threadIdx.x; c < 16 * MT * (K / 8); c += 512) {
+    const int r = c / (K / 8), k = (c % (K / 8)) * 8;
+    *reinterpret_cast<u32x4*>(As + r * P + k) =
+        *reinterpret_cast<const u32x4*>(g.a + int64_t(min(r, g.M - 1)) * g.sam + k);
+  }
+  const int nw = gridDim.x * 8, ntiles = (g.N + 15) / 16;
+  const int fr = lane % 16, fk = (lane / 16) * 8;
+  auto wrow = [&](int tile) { return g.w + int64_t(min(16 * tile + fr, g.N - 1)) * g.swn + fk; };
+  int tile = blockIdx.x * 8 + wave;
+  bf16x8_t b0[HS], b1[HS];
+  if (tile < ntiles) {
+    const uint16_t* w = wrow(tile);
+#pragma unroll
+    for (int k = 0; k < HS; ++k) b0[k] = *reinterpret_cast<const bf16x8_t*>(w + 32 * k);
+  }
+  __syncthreads();
+  // one half tile: MFMAs over k steps k0 .. k0 + 15 with W fragments b, the A fragments read 4 k steps at a time
+  // (the scheduling barrier keeps the compiler from reading all of them ahead into registers the W fragments in
+  // flight need)
+  auto half = [&](f32x4_t* acc, const bf16x8_t* b, int k0) {
+#pragma unroll
+    for (int k4 = 0; k4 < HS; k4 += 4) {
+      bf16x8_t av[4][MT];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          av[k][t] = *reinterpret_cast<const bf16x8_t*>(As + (16 * t + fr) * P + 32 * (k0 + k4 + k) + fk);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[k][t], b[k4 + k], acc[t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (; tile < ntiles; tile += nw) {
+    const uint16_t* w = wrow(tile);
+#pragma unroll
+    for (int k = 0; k < HS; ++k) b1[k] = *reinterpret_cast<const bf16x8_t*>(w + 32 * (HS + k));
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{};
+    half(acc, b0, 0);
+    if (tile + nw < ntiles) {
+      const uint16_t* wn = wrow(tile + nw);
+#pragma unroll
+      for (int k = 0; k < HS; ++k) b0[k] = *reinterpret_cast<const bf16x8_t*>(wn + 32 * k);
+    }
+    half(acc, b1, HS);
+    // lane l, register r of row tile t holds C row 16 t + 4 (l / 16) + r, column 16 tile + l % 16
+    const int n = 16 * tile + fr;
+    if (n < g.N) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * t + 4 * (lane / 16) + r;
+          if (m < g.M) g.c[int64_t(m) * g.scm + n] = f32_to_bf16(acc[t][r]);
+        }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
 // RMSNorm (or Add+RMSNorm) of the A rows fused into the decode GEMM (M <= 32): the norm that precedes a projection
 // (input_layernorm -> qkv, post_attention_layernorm -> gate_up) in the same launch. Every block normalises the
 // 16 * MT rows it multiplies -- K = 256 * KC, half a wave per row, each lane the same KC 16-byte chunks and the
@@ -1154,11 +1233,17 @@ int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   // very wide outputs (the LM head): 64 columns per block, so each block's A reads serve four times the W bytes;
   // 4 waves (a sweep of 2 / 4 / 8 / 16 waves x 2 / 4 / 8 / 16 steps x 16 / 32 / 64 columns picked 4 waves of 8 k
   // steps for gemm_skinny: 32 x 151936 x 1024 in 73.6 us vs 81.0 us with 8 waves of 4); staged through LDS one
-  // 128-k round at a time (52 KB of LDS, three blocks per CU): 64.3 us (two k steps per wave and round: 86.7 us)
+  // 128-k round at a time (52 KB of LDS, three blocks per CU): 64.3 us (two k steps per wave and round: 86.7 us);
+  // with K = 1024 (the Qwen3-0.6B LM head) gemm_wide_k1024: A staged once per block, each wave streaming W tiles
+  // of 16 columns, 256 blocks of 8 waves
   if constexpr (!SILU)
     if ((nout + 63) / 64 >= 8 * kBlocks) {
-      const dim3 grid(unsigned((nout + 63) / 64), unsigned((g.M + 16 * MT - 1) / (16 * MT)));
-      hipLaunchKernelGGL((gemm_skinny_lds<MT, 64, 4, 1, SILU>), grid, dim3(4 * 64), 0, s, g);
+      if (g.K == 1024) {
+        hipLaunchKernelGGL((gemm_wide_k1024<MT>), dim3(256), dim3(512), 0, s, g);
+      } else {
+        const dim3 grid(unsigned((nout + 63) / 64), unsigned((g.M + 16 * MT - 1) / (16 * MT)));
+        hipLaunchKernelGGL((gemm_skinny_lds<MT, 64, 4, 1, SILU>), grid, dim3(4 * 64), 0, s, g);
+      }
       return check_launch("matmul");
     }
   if ((nout + 15) / 16 >= kBlocks) return launch_skinny_tile<MT, 16, SILU>(g, s);
