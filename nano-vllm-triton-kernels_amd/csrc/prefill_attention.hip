@@ -250,6 +250,26 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
     }
     if constexpr (PAGED) R.all = false;  // a block-table entry may be invalid
   };
+  // every key of the tile at kt0 is valid: the bases plus a per-tile offset (contiguous keys only)
+  auto gload_full = [&](Regs& R, int kt0) {
+    R.all = true;
+    R.kok = 0;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      R.k[i] = *reinterpret_cast<const u32x4*>(kbase[i] + int64_t(kt0) * g.k_st);
+      R.v[i] = *reinterpret_cast<const u32x4*>(vbase[i] + int64_t(kt0) * g.v_st);
+    }
+  };
+  auto lstore_full = [&](const Regs& R, int stage) {  // R holds a tile whose keys are all valid
+    uint16_t* Ks = lds + stage * STAGE;
+    uint16_t* Vs = Ks + kBK * KP;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int c = tid + i * NT;
+      *reinterpret_cast<u32x4*>(&Ks[(c / CPR) * KP + (c % CPR) * 8]) = R.k[i];
+      *reinterpret_cast<u32x4*>(&Vs[(c / CPR) * VP + (c % CPR) * 8]) = R.v[i];
+    }
+  };
   auto lstore = [&](const Regs& R, int stage) {
     uint16_t* Ks = lds + stage * STAGE;
     uint16_t* Vs = Ks + kBK * KP;
@@ -386,7 +406,20 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
     __syncthreads();
     gload(A, min(k_beg + kBK, last));
     int stage = 0;
-    for (int kt0 = k_beg; kt0 < k_stop; kt0 += kBK) {
+    int kt0 = k_beg;
+    if constexpr (!PAGED) {
+      // while the tile stored next and the one loaded next are both whole (every key valid), the loop body holds
+      // only their loads and stores: the general loader's per-key row arithmetic and the zeroing selects, which the
+      // compiler executes on every tile when the two paths share the body, are left to the last tiles
+      for (; kt0 < k_stop && min(kt0 + 2 * kBK, last) + kBK <= lk; kt0 += kBK) {
+        tile(kt0, stage);
+        lstore_full(A, stage ^ 1);
+        gload_full(A, min(kt0 + 2 * kBK, last));
+        __syncthreads();
+        stage ^= 1;
+      }
+    }
+    for (; kt0 < k_stop; kt0 += kBK) {
       tile(kt0, stage);
       lstore(A, stage ^ 1);
       gload(A, min(kt0 + 2 * kBK, last));
