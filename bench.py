@@ -127,6 +127,7 @@ def bench_lib():
     lib.nvhip_bench_stream_copy.argtypes = [p, p, i64, i, p]
     lib.nvhip_bench_stream_rw.argtypes = [p, p, i64, i, i, p]
     lib.nvhip_bench_qk_pattern.argtypes = [p, p, p, p, i64, i64, i64, p, p, p, i64, p, p, i64, i64, i64, i64, p]
+    lib.nvhip_bench_mfma_lds.argtypes = [i, i, i, i, p, p, p]
     return lib
 
 
@@ -229,6 +230,48 @@ def hbm_ceiling(torch, dev, table=False, moved=2 ** 30):
     if table:
         out["table"] = points
     return out
+
+
+def mfma_ceiling(torch, dev, iters=20000):
+    """The bf16 MFMA ceiling of this part (libnvhip_bench.so's nvhip_bench_mfma_lds): one block per CU whose waves
+    issue v_mfma_f32_32x32x16_bf16 back to back, with 0, 2, 4, 6 or 8 KB of LDS fragment reads per 8 MFMAs (a GEMM
+    wave tile of 64 x 64 reads 1 KB per MFMA, 64 x 128 0.75 KB, 128 x 128 0.5 KB), at 1, 2 or 4 waves per SIMD.
+    Per point, the best of 3 timed launches after 2 untimed ones: TFLOP/s over the launch (HIP events), the shader
+    clock (per-wave s_memtime cycles over s_memrealtime ticks) and the MFMA pipe's busy fraction per clock (a
+    32x32x16 MFMA holds a SIMD's pipe for 32 cycles)."""
+    lib = bench_lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream()
+    rows = []
+    for waves in (4, 8, 16):
+        clocks = torch.zeros(2 * cus * waves, dtype=torch.int64, device=dev)
+        sink = torch.empty(cus * waves * 64, dtype=torch.float32, device=dev)
+        for reads in (0, 2, 4, 6, 8):
+            def launch():
+                rc = lib.nvhip_bench_mfma_lds(reads, waves, iters, cus, clocks.data_ptr(), sink.data_ptr(),
+                                              stream.cuda_stream)
+                assert rc == 0, rc
+            for _ in range(2):
+                launch()
+            best = None
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                launch()
+                e1.record(stream)
+                e1.synchronize()
+                ms = e0.elapsed_time(e1)
+                c = clocks.view(-1, 2).double().mean(0).tolist()
+                pt = (ms, c[0], c[1])
+                best = pt if best is None or ms < best[0] else best
+            ms, cyc, ticks = best
+            flops = cus * waves * iters * 8 * 32 * 32 * 16 * 2
+            rows.append({"waves_per_simd": waves // 4, "lds_kb_per_mfma": reads / 8, "ms": round(ms, 4),
+                         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                         "frac_2p5": round(flops / (ms * 1e-3) / 2.5e15, 4),
+                         "clock_ghz": round(cyc / (ticks * 10.0), 3),
+                         "mfma_pipe_busy": round(iters * 8 * (waves // 4) * 32 / cyc, 4)})
+    return {"iters": iters, "blocks": cus, "points": rows}
 
 
 def time_graph(torch, fn, n_calls, steps, warmup, min_warm_s=0.0):
@@ -810,6 +853,9 @@ def main():
     p.add_argument("--hbm-sweep", action="store_true",
                    help="only the HBM ceiling sweep (read-only, write-only and copy streams), every point printed, "
                         "at 1 GiB per launch and at the headline's bytes per launch")
+    p.add_argument("--mfma-probe", action="store_true",
+                   help="only the bf16 MFMA ceiling probe (MFMA issue with 0-1 KB of LDS reads per MFMA, 1-4 waves "
+                        "per SIMD), every point printed")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: only one GPU is measured (the kernel path has no collective: under "
@@ -827,6 +873,9 @@ def main():
         print(json.dumps(hbm_ceiling(torch, dev, table=True)), flush=True)
         print(json.dumps(hbm_ceiling(torch, dev, table=True, moved=fused_bytes(args.tokens, args.tokens))),
               flush=True)
+        return
+    if args.mfma_probe:
+        print(json.dumps(mfma_ceiling(torch, dev)), flush=True)
         return
     if args.profile_gemm:
         profile_gemm(torch, kernels, dev, args.steps, args.gemm_m)

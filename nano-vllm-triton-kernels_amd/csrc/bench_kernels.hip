@@ -17,6 +17,11 @@
 //                            iteration issued before its stores), plain / nontemporal / written-through (sc1)
 //                            cache policy, a grid-stride grid of `blocks` 256-thread blocks or (blocks 0) a one-shot
 //                            grid with one iteration per block.
+//  nvhip_bench_mfma_lds      the bf16 MFMA ceiling: each wave issues 8 v_mfma_f32_32x32x16_bf16 per iteration (4
+//                            accumulators), with R of them each followed by a 16-byte-per-lane LDS read (R KB per
+//                            wave per iteration, R / 8 KB per MFMA) whose value is an operand of the next
+//                            iteration's MFMAs, as a GEMM's fragment reads feed its next k step; one block per CU
+//                            (96 KB of LDS), per-wave shader-clock and 100 MHz real-time counts around the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -158,7 +163,88 @@ void launch_sweep_u(int unroll, int pol, dim3 grid, hipStream_t s, u32x4* dst, c
   }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kProbeLds = 96 * 1024;   // dynamic LDS per block: one block per CU
+constexpr int kProbeSpan = 64 * 1024;  // bytes the reads cycle through
+
+template <int R>
+__global__ __launch_bounds__(1024) void mfma_lds_kernel(int iters, unsigned long long* __restrict__ clocks,
+                                                        float* __restrict__ sink) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  // bf16 values in [1, 2): the sums stay finite over any iteration count used here
+  for (int i = threadIdx.x; i < kProbeSpan / 4; i += blockDim.x)
+    reinterpret_cast<uint32_t*>(lds)[i] = 0x3f803f80u + ((i & 0x7f) << 16) + (i >> 7 & 0x7f);
+  __syncthreads();
+  bf16x8 f[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) f[m] = *reinterpret_cast<const bf16x8*>(lds + m * 1024 + lane * 16);
+  f32x16 c[4] = {};
+  __syncthreads();
+  const unsigned long long t0 = clock64(), w0 = wall_clock64();
+  for (int it = 0; it < iters; ++it) {
+    const uint32_t off = uint32_t(it * 8 + wave) * 1024u % kProbeSpan;
+    bf16x8 nf[R > 0 ? R : 1];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      c[m % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[m], f[(m + 1) % 8], c[m % 4], 0, 0, 0);
+      if (m < R) nf[m] = *reinterpret_cast<const bf16x8*>(lds + (off + m * 3072u) % kProbeSpan + lane * 16);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int m = 0; m < R; ++m) f[m] = nf[m];
+  }
+  const unsigned long long t1 = clock64(), w1 = wall_clock64();
+  float s = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += c[m][e];
+  sink[int64_t(blockIdx.x) * blockDim.x + threadIdx.x] = s;
+  if (lane == 0) {
+    const int64_t w = int64_t(blockIdx.x) * (blockDim.x / 64) + wave;
+    clocks[2 * w] = t1 - t0;
+    clocks[2 * w + 1] = w1 - w0;
+  }
+}
+
+template <int R>
+int launch_mfma_lds(int waves, int iters, int blocks, unsigned long long* clocks, float* sink, hipStream_t s) {
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_lds_kernel<R>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kProbeLds) != hipSuccess)
+      return -2;
+    attr = true;
+  }
+  hipLaunchKernelGGL(mfma_lds_kernel<R>, dim3(blocks), dim3(64 * waves), kProbeLds, s, iters, clocks, sink);
+  return 0;
+}
+
 }  // namespace
+
+// reads: LDS reads of 16 bytes per lane per 8 MFMAs (0, 2, 4, 6 or 8); waves per block 4, 8 or 16 (1, 2 or 4 per
+// SIMD). clocks: 2 x blocks x waves uint64 (shader clocks, 100 MHz ticks per wave); sink: blocks x 64 x waves floats.
+extern "C" int nvhip_bench_mfma_lds(int reads, int waves, int iters, int blocks, void* clocks, void* sink,
+                                    void* stream) {
+  if (!clocks || !sink || iters <= 0 || blocks <= 0 || (waves != 4 && waves != 8 && waves != 16)) return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto* c = static_cast<unsigned long long*>(clocks);
+  auto* k = static_cast<float*>(sink);
+  int rc;
+  switch (reads) {
+    case 0: rc = launch_mfma_lds<0>(waves, iters, blocks, c, k, s); break;
+    case 2: rc = launch_mfma_lds<2>(waves, iters, blocks, c, k, s); break;
+    case 4: rc = launch_mfma_lds<4>(waves, iters, blocks, c, k, s); break;
+    case 6: rc = launch_mfma_lds<6>(waves, iters, blocks, c, k, s); break;
+    case 8: rc = launch_mfma_lds<8>(waves, iters, blocks, c, k, s); break;
+    default: return -1;
+  }
+  if (rc) return rc;
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
 
 // bytes: the stream's length (read-only: bytes read; write-only: bytes written; copy: bytes read = bytes written),
 // a multiple of 16. dst must hold `bytes` (read-only: one 16-byte vector per thread of the grid, written only if
