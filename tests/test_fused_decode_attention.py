@@ -2,7 +2,8 @@
 (nvhip_qk_norm_rope_kv_decode_attention_bf16) on the GPU: bitwise qk_norm_rope_kv followed by
 flash_attn_with_kvcache -- the attention output and both caches -- at the Qwen3-0.6B attention shape with and
 without the context split of small batches, block sizes that do and do not hold whole 32-token chunks, head_dim
-64 with 4 q heads per kv head, padding slots, and the wrapper's fallback for head_dim 256."""
+64 with 4 q heads per kv head, padding slots, slots outside the decode layout, and the wrapper's fallback for
+head_dim 256."""
 import pytest
 import torch
 
@@ -80,6 +81,28 @@ def test_fallback_for_head_dim_256():
     got, ref, c1, c2 = both(case(lens, Hq=8, Hkv=2, D=256, bs=32, seed=6))
     assert torch.equal(got, ref)
     assert torch.equal(c1[0], c2[0]) and torch.equal(c1[1], c2[1])
+
+
+@pytest.mark.parametrize("B", [3, 32])
+def test_slot_in_another_sequences_context(B):
+    """A slot inside another sequence's context (B = 32: the length-balanced launch, whose blocks run pieces of
+    two pairs): the new rows still land in the cache bitwise as the two calls write them, and every sequence whose
+    context does not hold that slot gets the two calls' output bitwise. The sequence that reads the slot is
+    outside the guarantee (its block may run before or after the writing block), so only its finiteness is
+    checked."""
+    g = torch.Generator("cpu").manual_seed(40 + B)
+    lens = [300, 900, 45] if B == 3 else torch.randint(64, 2049, (B,), generator=g).tolist()
+    c = list(case(lens, seed=9 + B))
+    bt, slots = c[11].cpu(), c[5].clone()
+    bs = c[9].shape[1]
+    reader, writer, tok = 0, B - 1, 7
+    slots[writer] = int(bt[reader, tok // bs]) * bs + tok % bs
+    c[5] = slots
+    got, ref, c1, c2 = both(tuple(c))
+    assert torch.equal(c1[0], c2[0]) and torch.equal(c1[1], c2[1])
+    others = [b for b in range(B) if b != reader]
+    assert torch.equal(got[others], ref[others])
+    assert torch.isfinite(got[reader].float()).all()
 
 
 def test_graph_replay_matches_eager():
