@@ -508,10 +508,51 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& g, const Piece& p
   }
   __syncthreads();
   if (!*flag) return;
+  const float* recs = g.ws + int64_t(pair) * g.rec_splits * g.rec_stride;
+  constexpr int SMEM_FLOATS = (VBYTES > RBYTES ? VBYTES : RBYTES) / 4;
+  if (nsplit <= 8 || nsplit * rows * 2 > SMEM_FLOATS) {
+    for (int idx = threadIdx.x; idx < rows * D; idx += NWV * 64) {
+      const int r = idx / D, d = idx % D;
+      const float o = merge_splits<true>(recs + r * (2 + D), g.rec_stride, nsplit, 2 + d);
+      const int i = r / g.G, hh = r % g.G;
+      g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
+    }
+    return;
+  }
+  // many splits (a few long sequences): merge_splits' arithmetic with fewer round trips to memory -- every split's
+  // (max, sum) of every row comes into LDS with one round of device-scope loads, then each (row, dim) sums the
+  // splits' O in split order with 16 splits' loads in flight (merge_splits issues 8 at a time, in two passes)
+  float* ml = reinterpret_cast<float*>(smem);  // [split][row][max, sum]; the partial O are no longer needed
+  for (int i = threadIdx.x; i < nsplit * rows * 2; i += NWV * 64) {
+    const int sp = i / (rows * 2), r = (i / 2) % rows, c = i % 2;
+    ml[i] = __hip_atomic_load(const_cast<float*>(recs + sp * g.rec_stride + r * (2 + D) + c), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
   for (int idx = threadIdx.x; idx < rows * D; idx += NWV * 64) {
     const int r = idx / D, d = idx % D;
-    const float* rec = g.ws + int64_t(pair) * g.rec_splits * g.rec_stride + r * (2 + D);
-    const float o = merge_splits<true>(rec, g.rec_stride, nsplit, 2 + d);
+    float M = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, ml[(sp * rows + r) * 2]);
+    float num = 0.0f, den = 0.0f;
+    if (M != -INFINITY) {
+      for (int s0 = 0; s0 < nsplit; s0 += 16) {
+        float o[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          o[u] = s0 + u < nsplit ? __hip_atomic_load(const_cast<float*>(recs + (s0 + u) * g.rec_stride + r * (2 + D) +
+                                                                        2 + d),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (s0 + u >= nsplit) break;
+          const float f = exp2f(ml[((s0 + u) * rows + r) * 2] - M);
+          num = __builtin_fmaf(o[u], f, num);
+          den = __builtin_fmaf(ml[((s0 + u) * rows + r) * 2 + 1], f, den);
+        }
+      }
+    }
+    const float o = den > 0.0f ? num / den : 0.0f;
     const int i = r / g.G, hh = r % g.G;
     g.out[int64_t(q0 + i) * g.o_st + int64_t(kvh * g.G + hh) * g.o_sh + d] = f32_to_bf16(o);
   }
