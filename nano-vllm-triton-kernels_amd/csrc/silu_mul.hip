@@ -8,14 +8,17 @@
 // Fast path (n a multiple of 8, 16-byte aligned rows): the [rows, n/8] space of 8-element vectors is flattened;
 // a 256-thread block takes VPT runs of 256 consecutive vectors, each thread one vector per run (gate and up are
 // two 16-byte loads, the output one 16-byte nontemporal store). The row of a vector comes from a multiply-shift
-// division.
+// division. One vector per thread and plain (not nontemporal) loads: a sweep of 1 / 2 / 4 vectors per thread x
+// plain / nontemporal loads (graph replay over 8 rotating inputs) took T = 1 / 32 / 2048 / 8192 (gate_up 6144 wide)
+// from 3.12 / 3.28 / 9.26 / 27.17 us (2 vectors, nontemporal) to 2.73 / 3.06 / 8.71 / 26.86 us; 4 vectors per
+// thread was the slowest at every T (fewer blocks to spread the latency over).
 #include "common.h"
 
 namespace nvhip {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kVpt = 2;
+constexpr int kVpt = 1;
 
 // n / d and n % d for 0 <= n, d < 2^31 with one mulhi (round-up reciprocal; Granlund & Montgomery 1994, sec. 4).
 struct FastDiv {
@@ -49,8 +52,8 @@ __global__ __launch_bounds__(kBlock) void silu_mul_kernel(const SiluArgs a) {
     col[k] = (idx - row[k] * a.per_row.d) * 8;
     if (idx < a.total) {
       const uint16_t* xr = a.x + int64_t(row[k]) * a.x_stride + col[k];
-      gate[k] = load8_once<true>(xr);
-      up[k] = load8_once<true>(xr + a.n);
+      gate[k] = load8<true>(xr);
+      up[k] = load8<true>(xr + a.n);
     }
   }
 #pragma unroll
