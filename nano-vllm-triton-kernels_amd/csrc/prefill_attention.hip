@@ -218,6 +218,19 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
       vbase[i] = g.v + int64_t(k0s + c / CPR) * g.v_st + int64_t(kvh) * D + (c % CPR) * 8;
     }
   }
+  // PAGED: block-table entries of this thread's keys in the tile the next gload call loads (the tiles are loaded
+  // in order, the last one repeated), fetched one call ahead: the fetch is issued before that call's data loads and
+  // retires with them, so no tile's data loads wait for a block-table load (at 4 key tiles per block, a 256-token
+  // chunk over 3840 cached keys, that wait was a memory round trip per tile)
+  const int last = (k_stop - 1) / kBK * kBK;
+  int kblk_nx[NL];
+  auto bt_fetch = [&](int kt0) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int kj = kt0 + (tid + i * NT) / CPR;
+      kblk_nx[i] = kj < lk ? bt_row[kj / g.bs] : 0;
+    }
+  };
   auto gload = [&](Regs& R, int kt0) {
     R.all = kt0 + kBK <= lk;
     R.kok = 0;
@@ -231,13 +244,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
         return;
       }
     }
-    // block-table entries of this thread's keys first (PAGED), then every data load back to back
+    // block-table entries of this thread's keys (PAGED: fetched by the previous call), then the entries of the
+    // tile the next call loads, then every data load back to back
     int kblk[NL];
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int kj = kt0 + (tid + i * NT) / CPR;
-      kblk[i] = PAGED && kj < lk ? bt_row[kj / g.bs] : 0;
-    }
+    for (int i = 0; i < NL; ++i) kblk[i] = PAGED ? kblk_nx[i] : 0;
+    if constexpr (PAGED) bt_fetch(min(kt0 + kBK, last));
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * NT;
@@ -399,8 +411,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // stored into the other and the loads of tile i + 2 are issued; one barrier per tile. Past the last tile the last
   // one is loaded and stored again, unused (every load is issued unconditionally so the compiler's waits are exact).
   {
-    const int last = (k_stop - 1) / kBK * kBK;
     Regs A;
+    if constexpr (PAGED) bt_fetch(k_beg);
     gload(A, k_beg);
     lstore(A, 0);
     __syncthreads();
@@ -460,48 +472,78 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
 
 // Merges the split records of every query of the sequences the prefill kernel took, in split order:
 // O = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s; a query no split saw (M = -inf) is zero.
-// One wave per (query, head), 4 per block (block x: sequence x / per_seq, its (query, head) pairs 4 (x % per_seq)
-// ..): lane s < splits reads split s's max and sum (all at once), the weights are broadcast from those lanes, and
-// each lane sums D / 64 dims over the splits, four splits' loads in flight at a time.
+// One wave per two (query, head) pairs p0 = 2 w, p0 + 1 (pair = query * Hq + head; records of consecutive pairs are
+// adjacent), 4 waves per block (block x: sequence x / per_seq, its waves 4 (x % per_seq) ..): lane s < splits reads
+// split s's (max, sum) of both pairs (all at once), the weights come back to the whole wave with readlane, and half
+// h of the wave sums pair p0 + h, D / 32 dims per lane (one 16-byte load per split at D = 128), eight splits' loads
+// in flight at a time. (One wave per pair, 8-byte loads, four splits at a time: the merge of a 256-token chunk over
+// 3840 cached keys, 16 splits, read its 34.6 MB of records at ~5 TB/s.)
 template <int D>
 __global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int per_seq) {
-  constexpr int REC = record_len(D), DPL = D / 64;
+  constexpr int REC = record_len(D), DPL = D / 32, SB = 8;
+  static_assert(DPL == 2 || DPL == 4, "head_dim 64 or 128");
   const int b = blockIdx.x / per_seq;
-  const int pr = (blockIdx.x % per_seq) * 4 + int(threadIdx.x) / 64, lane = threadIdx.x % 64;
+  const int lane = threadIdx.x % 64, hh = lane / 32;
+  const int p0 = ((blockIdx.x % per_seq) * 4 + int(threadIdx.x) / 64) * 2;
   const int q0s = g.cu_q[b], lq = g.cu_q[b + 1] - q0s;
   if (lq <= g.lq_skip) return;  // the decode kernel wrote these rows (or there are none)
-  const int i = pr / g.Hq, h = pr % g.Hq;
-  if (i >= lq || q0s + i >= g.ws_rows) return;
+  const int64_t rows_left = min<int64_t>(lq, g.ws_rows - q0s);  // queries of the sequence that have records
+  const bool ok0 = p0 < rows_left * g.Hq, ok1 = p0 + 1 < rows_left * g.Hq;
+  if (!ok0) return;  // the wave's first pair is past the sequence's queries (wave-uniform)
   const int64_t step = g.ws_rows * g.Hq * REC;  // one split further
-  const float* rec = g.ws + (int64_t(q0s + i) * g.Hq + h) * REC;
+  const float* rec0 = g.ws + (int64_t(q0s) * g.Hq + p0) * REC;
   const bool mine = lane < g.splits;  // splits <= 64 (host)
-  const float m = mine ? rec[lane * step] : -INFINITY, l = mine ? rec[lane * step + 1] : 0.0f;
-  float M = m;
+  f32x2 ml0 = {-INFINITY, 0.0f}, ml1 = {-INFINITY, 0.0f};
+  if (mine) ml0 = *reinterpret_cast<const f32x2*>(rec0 + lane * step);
+  if (mine && ok1) ml1 = *reinterpret_cast<const f32x2*>(rec0 + REC + lane * step);
+  float M0 = ml0[0], M1 = ml1[0];
 #pragma unroll
-  for (int off = 32; off >= 1; off /= 2) M = fmaxf(M, __shfl_xor(M, off));
-  const float f = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);  // 0 for a split that saw nothing
-  float den = l * f;
+  for (int off = 32; off >= 1; off /= 2) M0 = fmaxf(M0, __shfl_xor(M0, off)), M1 = fmaxf(M1, __shfl_xor(M1, off));
+  const float f0 = M0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml0[0] - M0);  // 0 for a split that saw nothing
+  const float f1 = M1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml1[0] - M1);
+  float den0 = ml0[1] * f0, den1 = ml1[1] * f1;
 #pragma unroll
-  for (int off = 32; off >= 1; off /= 2) den += __shfl_xor(den, off);
+  for (int off = 32; off >= 1; off /= 2) den0 += __shfl_xor(den0, off), den1 += __shfl_xor(den1, off);
+  const bool mine_pair = hh == 0 || ok1;
+  const float* rp = rec0 + hh * REC + 4 + (lane % 32) * DPL;
   float num[DPL] = {};
-  for (int sp0 = 0; sp0 < g.splits; sp0 += 4) {
-    float v[4][DPL], fs[4];
+  for (int sp0 = 0; sp0 < g.splits; sp0 += SB) {
+    float v[SB][DPL];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < SB; ++u) {
       const int sp = min(sp0 + u, g.splits - 1);
-      fs[u] = sp0 + u < g.splits ? __shfl(f, sp) : 0.0f;
+      if (mine_pair) {
+        if constexpr (DPL == 4) {
+          const f32x4_t x = *reinterpret_cast<const f32x4_t*>(rp + sp * step);
+          v[u][0] = x[0], v[u][1] = x[1], v[u][2] = x[2], v[u][3] = x[3];
+        } else {
+          const f32x2 x = *reinterpret_cast<const f32x2*>(rp + sp * step);
+          v[u][0] = x[0], v[u][1] = x[1];
+        }
+      } else {
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) v[u][e] = rec[sp * step + 4 + lane * DPL + e];
+        for (int e = 0; e < DPL; ++e) v[u][e] = 0.0f;
+      }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < SB; ++u) {
+      if (sp0 + u >= g.splits) break;  // uniform
+      const float w0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f0), sp0 + u));
+      const float w1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f1), sp0 + u));
+      const float w = hh ? w1 : w0;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) num[e] = __builtin_fmaf(v[u][e], fs[u], num[e]);
+      for (int e = 0; e < DPL; ++e) num[e] = __builtin_fmaf(v[u][e], w, num[e]);
+    }
   }
+  if (!mine_pair) return;
+  const float den = hh ? den1 : den0;
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-  uint16_t* o = g.out + int64_t(q0s + i) * g.o_st + int64_t(h) * g.o_sh + lane * DPL;
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) o[e] = f32_to_bf16(num[e] * inv);
+  const int pr = p0 + hh, i = pr / g.Hq, h = pr % g.Hq;
+  uint16_t* o = g.out + int64_t(q0s + i) * g.o_st + int64_t(h) * g.o_sh + (lane % 32) * DPL;
+  if constexpr (DPL == 4)
+    *reinterpret_cast<u32x2*>(o) = u32x2{pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
+  else
+    *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(num[0] * inv, num[1] * inv);
 }
 
 // Key splits: only when the blocks of one pass (query tiles x sequences x head groups) leave CUs idle and the
@@ -714,7 +756,7 @@ extern "C" int nvhip_prefill_attention_bf16(void* out, const void* q, const void
 #undef NVHIP_PREFILL_LAUNCH
   if (int rc = check_launch("prefill_attention")) return rc;
   if (g.splits == 1) return NVHIP_OK;
-  const int64_t per_seq = (max_seqlen_q * Hq + 3) / 4;  // blocks of 4 (query, head) waves per sequence
+  const int64_t per_seq = (max_seqlen_q * Hq + 7) / 8;  // blocks of 4 waves of two (query, head) pairs per sequence
   if (num_seqs * per_seq > INT32_MAX) return invalid("prefill_attention: size too large");
   const dim3 cgrid(static_cast<unsigned>(num_seqs * per_seq));
   if (D == 64) hipLaunchKernelGGL((prefill_combine<64>), cgrid, dim3(256), 0, s, g, int(per_seq));
