@@ -410,15 +410,25 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // Two LDS stages: while the waves compute tile i from one, the loads of tile i + 1 (issued a tile earlier) are
   // stored into the other and the loads of tile i + 2 are issued; one barrier per tile. Past the last tile the last
   // one is loaded and stored again, unused (every load is issued unconditionally so the compiler's waits are exact).
+  // The first tile is peeled: the loads of tiles 0 and 1 both go out before the first wait, so tile 1's are in
+  // flight during the prologue and tile 0 (with one set of tile registers, tile 1's loads went out after tile 0's
+  // LDS store and were waited for after a single tile of work).
   {
     Regs A;
     if constexpr (PAGED) bt_fetch(k_beg);
     gload(A, k_beg);
-    lstore(A, 0);
+    {
+      Regs B;
+      gload(B, min(k_beg + kBK, last));
+      lstore(A, 0);
+      __syncthreads();
+      tile(k_beg, 0);
+      lstore(B, 1);
+    }
+    gload(A, min(k_beg + 2 * kBK, last));
     __syncthreads();
-    gload(A, min(k_beg + kBK, last));
-    int stage = 0;
-    int kt0 = k_beg;
+    int stage = 1;
+    int kt0 = k_beg + kBK;
     if constexpr (!PAGED) {
       // while the tile stored next and the one loaded next are both whole (every key valid), the loop body holds
       // only their loads and stores: the general loader's per-key row arithmetic and the zeroing selects, which the
