@@ -560,8 +560,9 @@ def extras(torch, oracle, kernels, dev, steps):
     del a, b
     # decode-sized GEMMs are weight-bandwidth bound: rotate over enough weight copies (>= 512 MiB) that every call
     # reads its weight from HBM, as a decode step over 28 layers does
-    for layer, (K, N) in GEMM_SHAPES.items():
-        M = 32
+    # M = 32 (a decode batch), and M = 64 for the long-K projections (a batch of 33-64 rows)
+    for layer, M in [(name, 32) for name in GEMM_SHAPES] + [("down", 64), ("o_proj", 64)]:
+        K, N = GEMM_SHAPES[layer]
         nw = -(-(512 * 2 ** 20) // (N * K * 2))
         a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
         w0 = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)

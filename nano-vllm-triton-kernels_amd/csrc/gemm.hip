@@ -1283,6 +1283,11 @@ template <bool SILU>
 int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   if (g.M <= 16) return launch_skinny<1, SILU>(g, s);
   if (g.M <= 32) return launch_skinny<2, SILU>(g, s);
+  // 33 .. 64 rows with a long K (o_proj, down_proj): the skinny kernels' 16- or 32-row tiles as grid rows (512
+  // blocks at N = 1024) instead of 16 or 32 64x64 tiles, each a chain of K / 64 k-tiles on one CU (a CU streams
+  // ~45-50 GB/s either way; M = 64: down 17.1 -> 8.x us, o_proj 11.6 -> 6.x us). A row's bits then depend only on
+  // its 16-row tile, as for M <= 32.
+  if (g.M <= 64 && g.K >= 2048) return launch_skinny<2, SILU>(g, s);
   const int nk = (g.K + kBK - 1) / kBK;
   if (g.K % kBK != 0) return launch_mfma_shape<1, true, SILU>(g, s);
   if (nk % 2 == 0) return launch_mfma_shape<2, false, SILU>(g, s);

@@ -85,7 +85,7 @@ def test_ieee_is_not_tf32():
 QWEN_SHAPES = {"qkv": (1024, 4096), "gate_up": (1024, 6144), "down": (3072, 1024), "o_proj": (2048, 1024)}
 
 
-@pytest.mark.parametrize("M", [32, 256, 2048])
+@pytest.mark.parametrize("M", [32, 48, 64, 256, 2048])
 @pytest.mark.parametrize("layer", list(QWEN_SHAPES))
 def test_qwen_projection_shapes(layer, M):
     K, N = QWEN_SHAPES[layer]
@@ -111,6 +111,24 @@ def test_rows_do_not_depend_on_the_tile_choice(layer):
     full = matmul(a, w.t())
     for M in (100, 256, 512):
         assert torch.equal(matmul(a[:M], w.t()), full[:M]), M
+
+
+@pytest.mark.parametrize("layer", ["down", "o_proj"])
+def test_long_k_up_to_64_rows_run_in_row_tiles(layer):
+    """33 to 64 rows with K >= 2048 run the decode kernels' 16-row tiles as grid rows, so a row's bits depend only
+    on its tile: rows of 48- and 64-row products equal those of the 32-row product and of each other (a batch padded
+    from 33 to 48 rows keeps its real rows), and the product is within the bf16 tolerance of fp64."""
+    K, N = QWEN_SHAPES[layer]
+    g = torch.Generator("cpu").manual_seed(K * 3 + N)
+    a = (torch.randn(64, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    full = matmul(a, w.t())
+    assert torch.equal(matmul(a[:32], w.t()), full[:32])
+    assert torch.equal(matmul(a[:48], w.t()), full[:48])
+    padded = torch.cat([a[:33], torch.zeros(15, K, dtype=a.dtype, device=DEV)])
+    assert torch.equal(matmul(padded, w.t())[:33], matmul(a[:33], w.t()))
+    ref = oracle.matmul_fp64(a.cpu(), w.cpu().t())
+    torch.testing.assert_close(full.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("M", [1, 17, 32])
