@@ -1283,11 +1283,21 @@ template <bool SILU>
 int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   if (g.M <= 16) return launch_skinny<1, SILU>(g, s);
   if (g.M <= 32) return launch_skinny<2, SILU>(g, s);
-  // 33 .. 64 rows with a long K (o_proj, down_proj): the skinny kernels' 16- or 32-row tiles as grid rows (512
-  // blocks at N = 1024) instead of 16 or 32 64x64 tiles, each a chain of K / 64 k-tiles on one CU (a CU streams
-  // ~45-50 GB/s either way; M = 64: down 17.1 -> 8.x us, o_proj 11.6 -> 6.x us). A row's bits then depend only on
-  // its 16-row tile, as for M <= 32.
+  // Up to 256 rows with a long K (o_proj, down_proj): a block streams ~45-50 GB/s from L2 / HBM whatever the
+  // kernel, so the time is the bytes of the busiest block. The skinny kernels' row tiles as grid rows beat 16 - 64
+  // 64x64 tiles of K / 64 k-tiles each -- 33 .. 64 rows as for M <= 32 (512 blocks at N = 1024; M = 64: down 17.1
+  // -> 8.6 us, o_proj 11.7 -> 6.7 us), then 32-row x 16-column blocks while they fit one round (M = 128: 16.4 ->
+  // 11.1 / 11.3 -> 7.9 us), then 32 x 32 (M = 256: 15.9 -> 14.3 / 11.2 -> 9.9 us; 64-row blocks measured slower).
+  // A row's bits depend only on its tile's rows, as for M <= 32: every skinny block shape sums an output in the
+  // same k order.
   if (g.M <= 64 && g.K >= 2048) return launch_skinny<2, SILU>(g, s);
+  if constexpr (!SILU) {
+    const int64_t rows32 = (g.M + 31) / 32;
+    if (g.M <= 256 && g.K >= 2048) {
+      if (rows32 * ((g.N + 15) / 16) <= 256) return launch_skinny_tile<2, 16, SILU>(g, s);
+      if (rows32 * ((g.N + 31) / 32) <= 256) return launch_skinny_tile<2, 32, SILU>(g, s);
+    }
+  }
   const int nk = (g.K + kBK - 1) / kBK;
   if (g.K % kBK != 0) return launch_mfma_shape<1, true, SILU>(g, s);
   if (nk % 2 == 0) return launch_mfma_shape<2, false, SILU>(g, s);

@@ -54,12 +54,13 @@ def test_matmul(M, N, K, dtype, prec, b_transposed):
     check(a, b, prec, TOL[(dtype, prec)])
 
 
-@pytest.mark.parametrize("M,N,K", [(33, 4096, 1024), (100, 1024, 3072), (256, 6144, 1024), (2048, 4096, 1024),
+@pytest.mark.parametrize("M,N,K", [(33, 4096, 1024), (300, 1024, 3072), (256, 6144, 1024), (2048, 4096, 1024),
                                    (2048, 1024, 2048), (300, 200, 136), (65, 1000, 1000), (64, 8, 8)])
 def test_n_contiguous_b_is_bitwise_the_k_contiguous_product(M, N, K):
     """bf16 with B row-major ([K, N], N-contiguous: the reference test's layout) runs the MFMA tile kernel with B
-    staged as it lies and read through transpose reads; for M > 32 the K-contiguous layout of the same B runs the
-    same tile shape and k order, so the two products are bitwise equal (and within the bf16 tolerance of fp64).
+    staged as it lies and read through transpose reads; for M > 32 (M > 256 when K >= 2048) the K-contiguous layout
+    of the same B runs the same tile shape and k order, so the two products are bitwise equal (and within the bf16
+    tolerance of fp64).
     Covers N not a multiple of the tile (column clamp), K not a multiple of 64 (zero tail) and a strided B."""
     g = torch.Generator("cpu").manual_seed(M + N + K)
     a = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
@@ -100,15 +101,26 @@ def test_qwen_projection_shapes(layer, M):
 
 @pytest.mark.parametrize("layer", list(QWEN_SHAPES))
 def test_rows_do_not_depend_on_the_tile_choice(layer):
-    """Above 64 rows every MFMA tile shape (64x64 with 4 k-tiles of loads in flight while 64x64 tiles fit one round
-    on the CUs, the cost model's larger tiles beyond) sums each output in the same k order, so a row of C has the
-    same bits whatever M selects: rows of products with 100, 256 and 512 rows equal those rows of the 2048-row
-    product."""
+    """Every MFMA tile shape (64x64 with 4 k-tiles of loads in flight while 64x64 tiles fit one round on the CUs,
+    the cost model's larger tiles beyond) sums each output in the same k order, so a row of C has the same bits
+    whatever M selects: rows of products with 100, 256 and 512 rows equal those rows of the 2048-row product. With
+    K >= 2048 (down, o_proj) up to 256 rows run the skinny kernels' row tiles instead, whose block shapes also share
+    one k order: there rows of 100- and 256-row products equal those of the 64-row product, and 512 rows equal the
+    2048-row product."""
     K, N = QWEN_SHAPES[layer]
     g = torch.Generator("cpu").manual_seed(K + N)
     a = (torch.randn(2048, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
     w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
     full = matmul(a, w.t())
+    if K >= 2048:
+        assert torch.equal(matmul(a[:512], w.t()), full[:512])
+        rows64 = matmul(a[:64], w.t())
+        for M in (100, 256):
+            c = matmul(a[:M], w.t())
+            assert torch.equal(c[:64], rows64), M
+            ref = oracle.matmul_fp64(a[:M].cpu(), w.cpu().t())
+            torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
+        return
     for M in (100, 256, 512):
         assert torch.equal(matmul(a[:M], w.t()), full[:M]), M
 
