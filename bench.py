@@ -560,12 +560,15 @@ def extras(torch, oracle, kernels, dev, steps):
     del a, b
     # decode-sized GEMMs are weight-bandwidth bound: rotate over enough weight copies (>= 512 MiB) that every call
     # reads its weight from HBM, as a decode step over 28 layers does
-    # M = 32 (a decode batch), and M = 64 for the long-K projections (a batch of 33-64 rows)
+    # M = 32 (a decode batch), and M = 64 for the long-K projections (a batch of 33-64 rows; their inputs from a
+    # generator of their own, so the extras after them see the same inputs as without them)
+    g64 = torch.Generator().manual_seed(64)
     for layer, M in [(name, 32) for name in GEMM_SHAPES] + [("down", 64), ("o_proj", 64)]:
         K, N = GEMM_SHAPES[layer]
         nw = -(-(512 * 2 ** 20) // (N * K * 2))
-        a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
-        w0 = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
+        gl = g if M == 32 else g64
+        a = (torch.randn(M, K, generator=gl) / K ** 0.5).to(torch.bfloat16).to(dev)
+        w0 = torch.randn(N, K, generator=gl).to(torch.bfloat16).to(dev)
         ws = [w0.clone() for _ in range(nw)]
         ms, _ = time_graph(torch, lambda i: kernels.matmul(a, ws[i].t()), nw, max(nw, steps), nw, WARM_S)
         ms_ref, _ = time_graph(torch, lambda i: torch.nn.functional.linear(a, ws[i]), nw, max(nw, steps), nw, WARM_S)
