@@ -1289,14 +1289,14 @@ int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   // -> 8.6 us, o_proj 11.7 -> 6.7 us), then 32-row x 16-column blocks while they fit one round (M = 128: 16.4 ->
   // 11.1 / 11.3 -> 7.9 us), then 32 x 32 (M = 256: 15.9 -> 14.3 / 11.2 -> 9.9 us; 64-row blocks measured slower).
   // A row's bits depend only on its tile's rows, as for M <= 32: every skinny block shape sums an output in the
-  // same k order.
+  // same k order. The choice between the skinny and the tile kernels depends only on M, K and the W rows (g.N, gate
+  // and up rows together with SILU), so the SiLU x Mul epilogue runs the kernel family its two-step equivalent runs
+  // (the plain product of the same W) and stays bitwise equal to it.
   if (g.M <= 64 && g.K >= 2048) return launch_skinny<2, SILU>(g, s);
-  if constexpr (!SILU) {
-    const int64_t rows32 = (g.M + 31) / 32;
-    if (g.M <= 256 && g.K >= 2048) {
-      if (rows32 * ((g.N + 15) / 16) <= 256) return launch_skinny_tile<2, 16, SILU>(g, s);
-      if (rows32 * ((g.N + 31) / 32) <= 256) return launch_skinny_tile<2, 32, SILU>(g, s);
-    }
+  const int64_t rows32 = (g.M + 31) / 32;
+  if (g.M <= 256 && g.K >= 2048 && rows32 * ((g.N + 31) / 32) <= 256) {
+    if (SILU || rows32 * ((g.N + 15) / 16) <= 256) return launch_skinny_tile<2, 16, SILU>(g, s);
+    return launch_skinny_tile<2, 32, SILU>(g, s);
   }
   const int nk = (g.K + kBK - 1) / kBK;
   if (g.K % kBK != 0) return launch_mfma_shape<1, true, SILU>(g, s);

@@ -231,11 +231,12 @@ def test_golden_small():
         torch.testing.assert_close(matmul(ab, wb.t()).cpu().double(), refb, rtol=1.6e-2, atol=1e-2 * math.sqrt(K))
 
 
-@pytest.mark.parametrize("M", [1, 5, 16, 17, 32, 33, 64, 100, 2048])
-@pytest.mark.parametrize("I,K", [(3072, 1024), (40, 64), (300, 136)])
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 32, 33, 64, 100, 256, 2048])
+@pytest.mark.parametrize("I,K", [(3072, 1024), (40, 64), (300, 136), (1024, 2048), (512, 3072)])
 def test_matmul_silu_mul_is_bitwise_the_two_step_result(M, I, K):
     """The fused gate_up + SiLU x Mul equals silu_and_mul(matmul(x, w.t())) bit for bit (same per-column k order,
-    same rounding points); the two-step result itself is checked against the oracle elsewhere."""
+    same rounding points; K >= 2048 covers the skinny kernels' row tiles up to 256 rows, which both calls pick from
+    M, K and the W rows alike); the two-step result itself is checked against the oracle elsewhere."""
     from nanovllm_hip.kernels import matmul_silu_and_mul, silu_and_mul
     g = torch.Generator("cpu").manual_seed(M * 7 + I)
     x = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
