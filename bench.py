@@ -809,13 +809,18 @@ def profile_gemm(torch, kernels, dev, steps, M):
     for layer, (K, N) in GEMM_SHAPES.items():
         a = (torch.randn(M, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
         w0 = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
-        # small M is weight-bandwidth bound: rotate over >= 512 MiB of weight copies so each call reads from HBM
-        ws = [w0.clone() for _ in range(-(-(512 * 2 ** 20) // (N * K * 2)))] if M <= 64 else [w0]
+        # up to a few hundred rows the weight stream matters: rotate over >= 512 MiB of weight copies so each call
+        # reads its weight from HBM, as a step over 28 layers does
+        ws = [w0.clone() for _ in range(-(-(512 * 2 ** 20) // (N * K * 2)))] if M <= 256 else [w0]
+        # all of ours, then all of torch's: neither reads a weight copy the other has just brought into the caches
         for i in range(steps):
             kernels.matmul(a, ws[i % len(ws)].t())
+        torch.cuda.synchronize()
+        for i in range(steps):
             torch.nn.functional.linear(a, ws[i % len(ws)])
         torch.cuda.synchronize()
-        print(f"profile: {steps} x matmul + F.linear, {layer} {M}x{N}x{K}, {len(ws)} weight copies", flush=True)
+        print(f"profile: {steps} x matmul, then {steps} x F.linear, {layer} {M}x{N}x{K}, {len(ws)} weight copies",
+              flush=True)
         del ws, w0, a
 
 

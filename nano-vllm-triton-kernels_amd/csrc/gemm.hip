@@ -1283,21 +1283,33 @@ template <bool SILU>
 int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   if (g.M <= 16) return launch_skinny<1, SILU>(g, s);
   if (g.M <= 32) return launch_skinny<2, SILU>(g, s);
-  // Up to 256 rows with a long K (o_proj, down_proj): a block streams ~45-50 GB/s from L2 / HBM whatever the
-  // kernel, so the time is the bytes of the busiest block. The skinny kernels' row tiles as grid rows beat 16 - 64
-  // 64x64 tiles of K / 64 k-tiles each -- 33 .. 64 rows as for M <= 32 (512 blocks at N = 1024; M = 64: down 17.1
-  // -> 8.6 us, o_proj 11.7 -> 6.7 us), then 32-row x 16-column blocks while they fit one round (M = 128: 16.4 ->
-  // 11.1 / 11.3 -> 7.9 us), then 32 x 32 (M = 256: 15.9 -> 14.3 / 11.2 -> 9.9 us; 64-row blocks measured slower).
-  // A row's bits depend only on its tile's rows, as for M <= 32: every skinny block shape sums an output in the
-  // same k order. The choice between the skinny and the tile kernels depends only on M, K and the W rows (g.N, gate
-  // and up rows together with SILU), so the SiLU x Mul epilogue runs the kernel family its two-step equivalent runs
-  // (the plain product of the same W) and stays bitwise equal to it.
-  if (g.M <= 64 && g.K >= 2048) return launch_skinny<2, SILU>(g, s);
+  // 33 .. 256 rows with a long K (o_proj, down_proj): a block streams ~45-50 GB/s from L2 / HBM whatever the
+  // kernel, so the time is the bytes of the busiest block, and 16 - 64 64x64 tiles, each a chain of K / 64 k-tiles
+  // on one CU, leave most CUs idle. There the skinny kernel runs 32-row blocks as grid rows, 16 columns wide while
+  // that grid fits one round on the CUs, else 32, its operands staged through LDS in rounds of 768 (16 columns) or
+  // 512 k (row-contiguous loads; read straight into fragments the same blocks took 11.1 vs 7.7 us at M = 128 and
+  // 14.3 vs 10.0 us at M = 256 for down_proj). Graph replay, weights from HBM, N = 1024, against the 64x64 tiles:
+  // M = 64 down 17.1 -> 7.8 us, o_proj 11.7 -> 6.4; M = 128 16.4 -> 7.7 / 11.3 -> 6.3; M = 256 15.9 -> 9.9 /
+  // 11.2 -> 8.3 (hipBLASLt 11.9 / 10.7, 9.6 / 10.5, 10.1 / 10.7). A row's bits depend only on its tile's rows, as for M <= 32: every
+  // skinny block shape sums an output in the same k order. The choice between the skinny and the tile kernels
+  // depends only on M, K and the W rows (g.N, gate and up rows together with SILU), so the SiLU x Mul epilogue runs
+  // the kernel family its two-step equivalent (the plain product of the same W) runs and stays bitwise equal to it.
   const int64_t rows32 = (g.M + 31) / 32;
   if (g.M <= 256 && g.K >= 2048 && rows32 * ((g.N + 31) / 32) <= 256) {
-    if (SILU || rows32 * ((g.N + 15) / 16) <= 256) return launch_skinny_tile<2, 16, SILU>(g, s);
-    return launch_skinny_tile<2, 32, SILU>(g, s);
+    const dim3 block(512);
+    if constexpr (SILU) {  // gate and up rows: 16 output columns stage 64 rows, as 32 plain columns do
+      hipLaunchKernelGGL((gemm_skinny_lds<2, 16, 8, 2, true>), dim3(unsigned((g.N / 2 + 15) / 16), unsigned(rows32)),
+                         block, 0, s, g);
+    } else if (rows32 * ((g.N + 15) / 16) <= 256) {
+      hipLaunchKernelGGL((gemm_skinny_lds<2, 16, 8, 3, false>), dim3(unsigned((g.N + 15) / 16), unsigned(rows32)),
+                         block, 0, s, g);
+    } else {
+      hipLaunchKernelGGL((gemm_skinny_lds<2, 32, 8, 2, false>), dim3(unsigned((g.N + 31) / 32), unsigned(rows32)),
+                         block, 0, s, g);
+    }
+    return check_launch("matmul");
   }
+  if (g.M <= 64 && g.K >= 2048) return launch_skinny<2, SILU>(g, s);  // wider outputs: the M <= 32 tilings
   const int nk = (g.K + kBK - 1) / kBK;
   if (g.K % kBK != 0) return launch_mfma_shape<1, true, SILU>(g, s);
   if (nk % 2 == 0) return launch_mfma_shape<2, false, SILU>(g, s);
