@@ -733,15 +733,27 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
   constexpr int NT = NCOL >= 16 ? NCOL / 16 : 1;
   static_assert(NCOL == 8 || NCOL == 16 || NCOL == 32, "output columns per block");
   static_assert(U >= 1 && U * 32 * NW == K, "one round of k steps");
-  __shared__ __attribute__((aligned(16))) uint16_t As[R * KP];
-  __shared__ float red[NW][NP][NT][MT][4][64];
+  // LDS: the normalised rows, then the block's W rows (staged with row-contiguous loads), whose bytes the
+  // cross-wave reduction reuses once every wave has read its W fragments
+  // (when they fit: not the K = 2048 tiles, which read their W fragments straight from memory)
+  constexpr int RW = NP * NCOL;                  // staged W rows: product p, column c at row p * NCOL + c
+  constexpr int WCH = RW * (K / 8), WCT = (WCH + 511) / 512;  // 16-byte W chunks, per thread
+  static_assert(WCH % 512 == 0, "whole W chunks per thread");
+  constexpr int A_BYTES = R * KP * 2, RED_BYTES = NW * NP * NT * MT * 4 * 64 * 4;
+  constexpr bool STAGE_W = A_BYTES + RW * KP * 2 <= 160 * 1024;
+  constexpr int W_BYTES = STAGE_W ? RW * KP * 2 : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[A_BYTES + (W_BYTES > RED_BYTES ? W_BYTES : RED_BYTES)];
+  uint16_t* As = reinterpret_cast<uint16_t*>(lds);
+  uint16_t* Ws = reinterpret_cast<uint16_t*>(lds + A_BYTES);
+  auto red = reinterpret_cast<float (*)[NP][NT][MT][4][64]>(lds + A_BYTES);
   const MfmaArgs& g = a.g;
   const int n0 = blockIdx.x * NCOL, m0 = blockIdx.y * R;
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int fr = lane % 16, fk = (lane / 16) * 8;
   const int nout = SILU ? g.N / 2 : g.N;
 
-  bf16x8_t wf[U][NP][NT];  // W fragments of the whole K (wave w: k steps w, w + NW, ...)
+  u32x4 wst[STAGE_W ? WCT : 1];  // STAGE_W: this thread's W chunks, chunk c = tid + 512 i, staged row c / (K / 8)
+  bf16x8_t wfd[STAGE_W ? 1 : U][NP][NT];  // else the W fragments of the whole K (wave w: k steps w, w + NW, ...)
 
   // the block's rows, normalised, into LDS: half h = lane / 32 of wave w takes rows w + (2 i + h) NW, lane
   // j = lane % 32 the chunks at elements 8 j + 256 k (rows past M are computed from row M - 1 and stored as zeros,
@@ -763,17 +775,27 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
   }
 #pragma unroll
   for (int k = 0; k < KC; ++k) wraw[k] = load8<true>(a.nw + 256 * k + cj);
-  // then the W fragments: loads return in issue order, so the rows' loads come in first and the norm below runs
-  // while the weight is still on its way from HBM (issued the other way round, every row load waited for the
-  // weight's: qkv + Add+RMSNorm at M = 32 6.66 -> 6.37 us, gate_up + SiLU 8.44 -> 8.06 us)
+  // then the W rows: loads return in issue order, so the rows' loads come in first and the norm below runs while
+  // the weight is still on its way from HBM (issued the other way round, every row load waited for the weight's:
+  // qkv + Add+RMSNorm at M = 32 6.66 -> 6.37 us, gate_up + SiLU 8.44 -> 8.06 us). 16-byte loads along the rows (32
+  // lanes cover 512 contiguous bytes) into LDS, not fragments straight from memory (16 rows x 64 bytes per
+  // instruction, half a 128-byte line each).
+  if constexpr (STAGE_W) {
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int wn = min(n0 + 16 * j + (NCOL == 8 ? fr % 8 : fr), nout - 1);
+    for (int i = 0; i < WCT; ++i) {
+      const int c = threadIdx.x + 512 * i, row = c / (K / 8), p = row / NCOL, wn = min(n0 + row % NCOL, nout - 1);
+      wst[i] = *reinterpret_cast<const u32x4*>(g.w + int64_t(p == 0 ? wn : nout + wn) * g.swn + (c % (K / 8)) * 8);
+    }
+  } else {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const uint16_t* wrow = g.w + int64_t(p == 0 ? wn : nout + wn) * g.swn + fk;
+    for (int j = 0; j < NT; ++j) {
+      const int wn = min(n0 + 16 * j + (NCOL == 8 ? fr % 8 : fr), nout - 1);
 #pragma unroll
-      for (int u = 0; u < U; ++u) wf[u][p][j] = *reinterpret_cast<const bf16x8_t*>(wrow + (wave + u * NW) * 32);
+      for (int p = 0; p < NP; ++p) {
+        const uint16_t* wrow = g.w + int64_t(p == 0 ? wn : nout + wn) * g.swn + fk;
+#pragma unroll
+        for (int u = 0; u < U; ++u) wfd[u][p][j] = *reinterpret_cast<const bf16x8_t*>(wrow + (wave + u * NW) * 32);
+      }
     }
   }
 #pragma unroll
@@ -805,6 +827,13 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
       *reinterpret_cast<u32x4*>(dst + 256 * k + cj) = m < g.M ? pack8(o) : u32x4{0, 0, 0, 0};
     }
   }
+  if constexpr (STAGE_W) {
+#pragma unroll
+    for (int i = 0; i < WCT; ++i) {
+      const int c = threadIdx.x + 512 * i;
+      *reinterpret_cast<u32x4*>(Ws + (c / (K / 8)) * KP + (c % (K / 8)) * 8) = wst[i];
+    }
+  }
   __syncthreads();
 
   f32x4_t acc[NP][NT][MT];
@@ -820,14 +849,25 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
     bf16x8_t af[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) af[t] = *reinterpret_cast<const bf16x8_t*>(As + (t * 16 + fr) * KP + k + fk);
+    bf16x8_t wf[NP][NT];  // with NCOL = 8 the MFMA's columns 8..15 repeat columns 0..7
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if constexpr (STAGE_W)
+          wf[p][j] = *reinterpret_cast<const bf16x8_t*>(Ws + (p * NCOL + (NCOL == 8 ? fr % 8 : 16 * j + fr)) * KP + k + fk);
+        else
+          wf[p][j] = wfd[u][p][j];
+      }
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int t = 0; t < MT; ++t)
-          acc[p][j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], wf[u][p][j], acc[p][j][t], 0, 0, 0);
+          acc[p][j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], wf[p][j], acc[p][j][t], 0, 0, 0);
   }
+  if constexpr (STAGE_W) __syncthreads();  // every wave has read its W fragments: the reduction reuses their bytes
 #pragma unroll
   for (int p = 0; p < NP; ++p)
 #pragma unroll
