@@ -1241,14 +1241,23 @@ int launch_mfma_bnm(const MfmaArgs& g, hipStream_t s) {
 // and every block reads all of its rows of A (32 x K: twice the W slice of a 16-column block), so narrow outputs
 // (N = 1024: 64 blocks of 32 x 16) need the smaller tiles to reach every CU.
 // 8-column blocks with K >= 2048 (o_proj, down_proj) stage their operands through LDS (gemm_skinny_lds, same bits):
-// o_proj 5.75 -> 4.58 us, down 7.81 -> 6.04 us with the weights from HBM; 16-column blocks and short K measured
-// within 4 % or slower that way (a barrier and an LDS round trip per round for little traffic).
+// o_proj 5.75 -> 4.58 us, down 7.81 -> 6.04 us with the weights from HBM. 16-column blocks with 512 < K <= 1024
+// (qkv, gate_up) stage the whole K in one round (every load of the block in flight at once, 16-byte loads along
+// the rows instead of fragments of half a 128-byte line per row): M = 32 qkv 5.38 -> 4.74 us, the 6144-wide gate_up
+// product 8.17 -> 7.61 us, M = 16 4.45 -> 4.25 / 6.28 -> 5.33 us (staged in rounds of 256 k they had measured
+// within 4 % or slower: a barrier and an LDS round trip per round).
 template <int MT, int NCOL, bool SILU>
 int launch_skinny_tile(const MfmaArgs& g, hipStream_t s) {
   constexpr int NW = 8;
   const int nout = SILU ? g.N / 2 : g.N;
   const dim3 grid(unsigned((nout + NCOL - 1) / NCOL), unsigned((g.M + 16 * MT - 1) / (16 * MT))), block(NW * 64);
   bool done = false;
+  if constexpr (NCOL == 16) {
+    if (g.K > 512 && g.K <= 1024) {  // the whole K in one round of up to 1024 (staged chunks past K are zero)
+      done = true;
+      hipLaunchKernelGGL((gemm_skinny_lds<MT, 16, NW, 4, SILU, true>), grid, block, 0, s, g);
+    }
+  }
   if constexpr (NCOL == 8 && MT == 1 && !SILU) {
     if (g.K >= 2048 && g.K <= 13 * 256) {  // the whole K in one round (24 staged rows: LDS <= 160 KB)
       done = true;

@@ -144,11 +144,12 @@ def test_long_k_up_to_64_rows_run_in_row_tiles(layer):
 
 
 @pytest.mark.parametrize("M", [1, 17, 32])
-@pytest.mark.parametrize("K", [1024, 2048, 2056, 3072, 4104])
+@pytest.mark.parametrize("K", [776, 1024, 2048, 2056, 3072, 4104])
 def test_decode_column_tilings_agree_bitwise(M, K):
     """M <= 32: the 8-wave block tilings sum a column in the same k order, so a column has the same bits in an
     8-column block (staged through LDS from K = 2048 on, N = 1024; K = 2056 / 4104 end in a partial round) and in a
-    16-column block with fragments loaded straight from memory (N = 4096); the 4-wave 64-column blocks of LM-head-wide outputs (staged through LDS) agree
+    16-column block (N = 4096: the whole K staged in one LDS round up to K = 1024, K = 776 ending inside it;
+    fragments loaded straight from memory beyond); the 4-wave 64-column blocks of LM-head-wide outputs (staged through LDS) agree
     with each other whatever the output width (151 936 = the Qwen3 vocabulary, 131 176 = 2049 blocks and a ragged one) and with the
     fp64 product."""
     g = torch.Generator(DEV).manual_seed(M * 131 + K)
