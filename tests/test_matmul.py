@@ -143,6 +143,20 @@ def test_long_k_up_to_64_rows_run_in_row_tiles(layer):
     torch.testing.assert_close(full.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("M,N,K", [(77, 1000, 2056), (200, 520, 4104), (45, 3000, 2048)])
+def test_long_k_row_tiles_ragged(M, N, K):
+    """The 33-256-row, K >= 2048 route on ragged sizes: rows past M, columns past N (not a multiple of the 16- or
+    32-column block), K ending inside a staged round; within the bf16 tolerance of fp64, and its first 32 rows
+    bitwise the 32-row product's (every skinny block shape sums a column in the same k order)."""
+    g = torch.Generator("cpu").manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    c = matmul(a, w.t())
+    ref = oracle.matmul_fp64(a.cpu(), w.cpu().t())
+    torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
+    assert torch.equal(c[:32], matmul(a[:32], w.t()))
+
+
 @pytest.mark.parametrize("M", [1, 17, 32])
 @pytest.mark.parametrize("K", [776, 1024, 2048, 2056, 3072, 4104])
 def test_decode_column_tilings_agree_bitwise(M, K):
