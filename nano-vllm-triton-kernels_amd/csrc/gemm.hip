@@ -627,79 +627,97 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
 // ------------------------------------------------------------------------------------------------------------
 // Wide decode outputs with K = 1024 (the tied LM head: 32 x 151 936 x 1024, a 311 MB weight): the block stages its
 // A rows (all M <= 32 of them, the whole K) in LDS once, and wave gw of the grid's nw takes the 16-column W tiles
-// gw, gw + nw, ... (neighbouring waves read neighbouring tiles): W fragments (16 bytes per lane per 32-wide k step)
-// loaded straight from memory, the second half of a tile and the first half of the next one in flight while a
-// half is multiplied, A fragments read from LDS four k steps at a time, v_mfma_f32_16x16x32_bf16 with the 32 k
-// steps of a tile accumulated in k order (no cross-wave sum). 151 936 x 1024 at M = 32, the weight from HBM:
-// 63.3 us against 67.1 us for the 64-column LDS-staged blocks (gemm_skinny_lds); with each wave taking a
-// contiguous range of tiles instead 67.6 us, with nontemporal W loads 71.0 us, with the A fragments kept in
-// registers (one wave per SIMD, 256 blocks of 4 waves) 73.2 us.
+// gw, gw + nw, ... (neighbouring waves read neighbouring tiles), v_mfma_f32_16x16x32_bf16 with the 32 k steps of a
+// tile accumulated in k order (no cross-wave sum), A fragments read from LDS four k steps at a time. Each wave
+// stages its tiles through its own LDS slice: a tile's 16 rows come in quarters of K (16 rows x 256 k, 8 KB) loaded
+// along the rows (two rows of 512 contiguous bytes per instruction) with the nontemporal hint, two quarters in
+// flight in registers while the wave multiplies the quarter in its slice. 151 936 x 1024 at M = 32, the weight from
+// HBM: 57.3 us against 63.6 us with the W fragments loaded straight from memory (16 rows x 64 bytes per
+// instruction, half a 128-byte line each; the same MFMAs in the same order, so the same bits); staged with plain
+// loads 65.8 us, three quarters in flight 57.5 us. Earlier variants of the fragment loads: 64-column LDS-staged
+// blocks (gemm_skinny_lds) 67.1 us, a contiguous range of tiles per wave 67.6 us, nontemporal fragment loads
+// 71.0 us, the A fragments kept in registers (one wave per SIMD) 73.2 us.
 template <int MT>
 __global__ __launch_bounds__(512) void gemm_wide_k1024(const MfmaArgs g) {
-  constexpr int KS = 32, HS = KS / 2, K = 1024, P = K + 8;  // row pitch: 16 rows of a fragment read on distinct banks
+  constexpr int DEPTH = 2;  // quarters in flight
+  constexpr int K = 1024, P = K + 8, Q = 256, QP = Q + 8, NQ = K / Q;
   __shared__ __attribute__((aligned(16))) uint16_t As[16 * MT * P];
+  __shared__ __attribute__((aligned(16))) uint16_t Wsl[8 * 16 * QP];
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   for (int c = threadIdx.x; c < 16 * MT * (K / 8); c += 512) {
     const int r = c / (K / 8), k = (c % (K / 8)) * 8;
     *reinterpret_cast<u32x4*>(As + r * P + k) =
         *reinterpret_cast<const u32x4*>(g.a + int64_t(min(r, g.M - 1)) * g.sam + k);
   }
-  const int nw = gridDim.x * 8, ntiles = (g.N + 15) / 16;
+  __syncthreads();  // the last block-wide step: the waves run on their own from here
+  const int nw = gridDim.x * 8, ntiles = (g.N + 15) / 16, tile0 = blockIdx.x * 8 + wave;
+  if (tile0 >= ntiles) return;
+  const int nunits = ((ntiles - 1 - tile0) / nw + 1) * NQ;  // (tile, quarter) units of this wave
   const int fr = lane % 16, fk = (lane / 16) * 8;
-  auto wrow = [&](int tile) { return g.w + int64_t(min(16 * tile + fr, g.N - 1)) * g.swn + fk; };
-  int tile = blockIdx.x * 8 + wave;
-  bf16x8_t b0[HS], b1[HS];
-  if (tile < ntiles) {
-    const uint16_t* w = wrow(tile);
+  uint16_t* ws = Wsl + wave * 16 * QP;
+  // unit u: tile tile0 + (u / NQ) nw, quarter u % NQ; instruction i loads rows 2 i + lane / 32, chunk lane % 32
+  auto qload = [&](u32x4 (&r)[8], int u) {
+    const int tile = tile0 + (u / NQ) * nw, q = u % NQ;
 #pragma unroll
-    for (int k = 0; k < HS; ++k) b0[k] = *reinterpret_cast<const bf16x8_t*>(w + 32 * k);
-  }
-  __syncthreads();
-  // one half tile: MFMAs over k steps k0 .. k0 + 15 with W fragments b, the A fragments read 4 k steps at a time
-  // (the scheduling barrier keeps the compiler from reading all of them ahead into registers the W fragments in
-  // flight need)
-  auto half = [&](f32x4_t* acc, const bf16x8_t* b, int k0) {
-#pragma unroll
-    for (int k4 = 0; k4 < HS; k4 += 4) {
-      bf16x8_t av[4][MT];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-          av[k][t] = *reinterpret_cast<const bf16x8_t*>(As + (16 * t + fr) * P + 32 * (k0 + k4 + k) + fk);
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[k][t], b[k4 + k], acc[t], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < 8; ++i) {
+      const int n = min(16 * tile + 2 * i + lane / 32, g.N - 1);
+      const u32x4* p = reinterpret_cast<const u32x4*>(g.w + int64_t(n) * g.swn + q * Q + (lane % 32) * 8);
+      r[i] = __builtin_nontemporal_load(p);  // read once
     }
   };
-  for (; tile < ntiles; tile += nw) {
-    const uint16_t* w = wrow(tile);
+  f32x4_t acc[MT];
+  auto unit = [&](u32x4 (&r)[8], int u) {
+    const int tile = tile0 + (u / NQ) * nw, q = u % NQ;
 #pragma unroll
-    for (int k = 0; k < HS; ++k) b1[k] = *reinterpret_cast<const bf16x8_t*>(w + 32 * (HS + k));
-    f32x4_t acc[MT];
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(ws + (2 * i + lane / 32) * QP + (lane % 32) * 8) = r[i];
+    if (u + DEPTH < nunits) qload(r, u + DEPTH);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (q == 0) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{};
-    half(acc, b0, 0);
-    if (tile + nw < ntiles) {
-      const uint16_t* wn = wrow(tile + nw);
-#pragma unroll
-      for (int k = 0; k < HS; ++k) b0[k] = *reinterpret_cast<const bf16x8_t*>(wn + 32 * k);
+      for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{};
     }
-    half(acc, b1, HS);
-    // lane l, register r of row tile t holds C row 16 t + 4 (l / 16) + r, column 16 tile + l % 16
-    const int n = 16 * tile + fr;
-    if (n < g.N) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
+    for (int k4 = 0; k4 < Q / 32; k4 += 4) {
+      bf16x8_t av[4][MT], wv[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * t + 4 * (lane / 16) + r;
-          if (m < g.M) g.c[int64_t(m) * g.scm + n] = f32_to_bf16(acc[t][r]);
-        }
+      for (int k = 0; k < 4; ++k) {
+        wv[k] = *reinterpret_cast<const bf16x8_t*>(ws + fr * QP + 32 * (k4 + k) + fk);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          av[k][t] = *reinterpret_cast<const bf16x8_t*>(As + (16 * t + fr) * P + q * Q + 32 * (k4 + k) + fk);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[k][t], wv[k], acc[t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // every lane has its fragments of this quarter (the MFMAs consumed them) before the slice is written again
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (q == NQ - 1) {  // lane l, register r of row tile t holds C row 16 t + 4 (l / 16) + r, column 16 tile + l % 16
+      const int n = 16 * tile + fr;
+      if (n < g.N) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int m = 16 * t + 4 * (lane / 16) + rr;
+            if (m < g.M) g.c[int64_t(m) * g.scm + n] = f32_to_bf16(acc[t][rr]);
+          }
+      }
+    }
+  };
+  u32x4 r0[8], r1[8];
+  qload(r0, 0);
+  if (nunits > 1) qload(r1, 1);
+  for (int u = 0; u < nunits; u += DEPTH) {
+    unit(r0, u);
+    if (u + 1 < nunits) unit(r1, u + 1);
   }
 }
 
@@ -1286,7 +1304,7 @@ int launch_skinny(const MfmaArgs& g, hipStream_t s) {
   // steps for gemm_skinny: 32 x 151936 x 1024 in 73.6 us vs 81.0 us with 8 waves of 4); staged through LDS one
   // 128-k round at a time (52 KB of LDS, three blocks per CU): 64.3 us (two k steps per wave and round: 86.7 us);
   // with K = 1024 (the Qwen3-0.6B LM head) gemm_wide_k1024: A staged once per block, each wave streaming W tiles
-  // of 16 columns, 256 blocks of 8 waves
+  // of 16 columns through its own LDS slice, 256 blocks of 8 waves
   if constexpr (!SILU)
     if ((nout + 63) / 64 >= 8 * kBlocks) {
       if (g.K == 1024) {
