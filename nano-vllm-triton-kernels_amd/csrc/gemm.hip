@@ -542,9 +542,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_lds(const MfmaArgs g) {
   u32x4 v[CPT];
   auto load_round = [&](int r) {
     const int k0 = r * KR;
+    // W rows (staged rows RA ..) are read once per launch: the nontemporal hint; the A rows, which every block
+    // reads, stay cached
 #pragma unroll
-    for (int i = 0; i < CPT; ++i)
-      v[i] = (live(i) && k0 + kof[i] < g.K) ? *reinterpret_cast<const u32x4*>(src[i] + k0) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < CPT; ++i) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(src[i] + k0);
+      const bool w_row = min(tid + NTH * i, NCH - 1) / CPR >= RA;
+      v[i] = (live(i) && k0 + kof[i] < g.K) ? (w_row ? __builtin_nontemporal_load(p) : *p) : u32x4{0, 0, 0, 0};
+    }
   };
   auto store_round = [&](int stage) {
 #pragma unroll
@@ -802,7 +807,10 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
 #pragma unroll
     for (int i = 0; i < WCT; ++i) {
       const int c = threadIdx.x + 512 * i, row = c / (K / 8), p = row / NCOL, wn = min(n0 + row % NCOL, nout - 1);
-      wst[i] = *reinterpret_cast<const u32x4*>(g.w + int64_t(p == 0 ? wn : nout + wn) * g.swn + (c % (K / 8)) * 8);
+      // read once per launch: the nontemporal hint (decode step 1712 -> 1692 us with the hint here and on the W rows
+      // of gemm_skinny_lds; alone, the launches time the same either way)
+      const uint16_t* wp = g.w + int64_t(p == 0 ? wn : nout + wn) * g.swn + (c % (K / 8)) * 8;
+      wst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp));
     }
   } else {
 #pragma unroll
