@@ -55,7 +55,7 @@ template <int LANES, int K, bool ADD, bool PART = false>
 __global__ __launch_bounds__(kBlock) void norm_kernel(const NormArgs a) {
   constexpr int N = LANES * K * 8, STRIDE = LANES * 8;
   const int sub = threadIdx.x % LANES;
-  const int64_t row = int64_t(blockIdx.x) * (kBlock / LANES) + threadIdx.x / LANES;
+  const int64_t row = int64_t(blockIdx.x) * (blockDim.x / LANES) + threadIdx.x / LANES;
   if (row >= a.rows) return;
 
   const uint16_t* xr;
@@ -221,9 +221,13 @@ __global__ __launch_bounds__(512) void norm_kernel_generic(const NormArgs a) {
 
 template <bool ADD, int LANES, int K, bool PART = false>
 int launch_fast(const NormArgs& a, hipStream_t s) {
-  const int64_t rows_per_block = kBlock / LANES;
+  // the split-K partials' sum (a mixed step's 256 rows of 4 x 4 KB of fp32 each): two rows per 64-thread block, so
+  // the rows spread over 4x the CUs (a block streams ~45-50 GB/s): mixed step 2212.6 -> 2169.6 us (one row per
+  // 32-thread block 2198 us)
+  const int threads = PART ? 2 * LANES : kBlock;
+  const int64_t rows_per_block = threads / LANES;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((norm_kernel<LANES, K, ADD, PART>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL((norm_kernel<LANES, K, ADD, PART>), dim3(unsigned(blocks)), dim3(threads), 0, s, a);
   return check_launch(ADD ? "add_rms_norm" : "rms_norm");
 }
 
