@@ -881,7 +881,8 @@ __global__ __launch_bounds__(512) void gemm_skinny_norm(const NormMfmaArgs a) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         if constexpr (STAGE_W)
-          wf[p][j] = *reinterpret_cast<const bf16x8_t*>(Ws + (p * NCOL + (NCOL == 8 ? fr % 8 : 16 * j + fr)) * KP + k + fk);
+          wf[p][j] = *reinterpret_cast<const bf16x8_t*>(Ws + (p * NCOL + (NCOL == 8 ? fr % 8 : 16 * j + fr)) * KP +
+                                                         k + fk);
         else
           wf[p][j] = wfd[u][p][j];
       }
@@ -1365,10 +1366,11 @@ int launch_mfma_auto(const MfmaArgs& g, hipStream_t s) {
   // 512 k (row-contiguous loads; read straight into fragments the same blocks took 11.1 vs 7.7 us at M = 128 and
   // 14.3 vs 10.0 us at M = 256 for down_proj). Graph replay, weights from HBM, N = 1024, against the 64x64 tiles:
   // M = 64 down 17.1 -> 7.8 us, o_proj 11.7 -> 6.4; M = 128 16.4 -> 7.7 / 11.3 -> 6.3; M = 256 15.9 -> 9.9 /
-  // 11.2 -> 8.3 (hipBLASLt 11.9 / 10.7, 9.6 / 10.5, 10.1 / 10.7). A row's bits depend only on its tile's rows, as for M <= 32: every
-  // skinny block shape sums an output in the same k order. The choice between the skinny and the tile kernels
-  // depends only on M, K and the W rows (g.N, gate and up rows together with SILU), so the SiLU x Mul epilogue runs
-  // the kernel family its two-step equivalent (the plain product of the same W) runs and stays bitwise equal to it.
+  // 11.2 -> 8.3 (hipBLASLt 11.9 / 10.7, 9.6 / 10.5, 10.1 / 10.7). A row's bits depend only on its tile's rows, as
+  // for M <= 32: every skinny block shape sums an output in the same k order. The choice between the skinny and the
+  // tile kernels depends only on M, K and the W rows (g.N, gate and up rows together with SILU), so the SiLU x Mul
+  // epilogue runs the kernel family its two-step equivalent (the plain product of the same W) runs and stays
+  // bitwise equal to it.
   const int64_t rows32 = (g.M + 31) / 32;
   if (g.M <= 256 && g.K >= 2048 && rows32 * ((g.N + 31) / 32) <= 256) {
     const dim3 block(512);

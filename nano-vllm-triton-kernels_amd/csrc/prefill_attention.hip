@@ -551,7 +551,8 @@ __global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int 
   const int pr = p0 + hh, i = pr / g.Hq, h = pr % g.Hq;
   uint16_t* o = g.out + int64_t(q0s + i) * g.o_st + int64_t(h) * g.o_sh + (lane % 32) * DPL;
   if constexpr (DPL == 4)
-    *reinterpret_cast<u32x2*>(o) = u32x2{pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
+    *reinterpret_cast<u32x2*>(o) =
+        u32x2{pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
   else
     *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(num[0] * inv, num[1] * inv);
 }
