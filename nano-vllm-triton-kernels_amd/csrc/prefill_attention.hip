@@ -66,7 +66,9 @@ struct PrefillArgs {
   int split_len;    // a multiple of kBK
   int Hq;
   int64_t ws_rows;  // Tq: query rows of one split's records
-  float* ws;        // splits > 1: [splits, Tq, Hq, D + 4] fp32 records (max, sum, -, -, O) merged by prefill_combine
+  // splits > 1: fp32 records merged by prefill_combine -- O [splits, Tq, Hq, D] (unnormalised), then (max, sum)
+  // [splits, Tq, Hq, 2]
+  float* ws;
   // dec_inline: the blocks of the short sequences (1 .. lq_skip queries) run their paged decode attention
   // themselves (one block per (sequence, kv head), dec: its varlen arguments, one split), concurrently with the
   // prefill tiles, instead of a separate launch before this one
@@ -77,8 +79,8 @@ struct PrefillArgs {
   DecodeArgs dec;
 };
 
-// fp32 elements of one (split, query, head) record: max, row sum, two unused (16-byte aligned O), O[D].
-__host__ __device__ constexpr int record_len(int D) { return D + 4; }
+// fp32 elements of one (split, query, head) record: O[D] in the O array, max and row sum in the (max, sum) array.
+__host__ __device__ constexpr int record_len(int D) { return D + 2; }
 
 // Element offset of key j of sequence b, kv head kvh, in k (v with v_st): a contiguous row, or (PAGED) the cache
 // slot of block blk (-1 if the block is not valid).
@@ -164,9 +166,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
       const int64_t row = q0s + qt * kBQ + r;
       if (g.splits > 1) {
         if (row >= g.ws_rows) return;
-        float* rec = g.ws + ((int64_t(split) * g.ws_rows + row) * g.Hq + h) * record_len(D);
-        rec[0] = -INFINITY;
-        for (int d = 1; d < record_len(D); ++d) rec[d] = 0.0f;
+        const int64_t rec = (int64_t(split) * g.ws_rows + row) * g.Hq + h;
+        float* o = g.ws + rec * D;
+        for (int d = 0; d < D; ++d) o[d] = 0.0f;
+        *reinterpret_cast<f32x2*>(g.ws + int64_t(g.splits) * g.ws_rows * g.Hq * D + 2 * rec) = f32x2{-INFINITY, 0.0f};
       } else {
         uint16_t* o = g.out + row * g.o_st + int64_t(h) * g.o_sh;
         for (int d = 0; d < D; ++d) o[d] = 0;
@@ -453,22 +456,47 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
   // row sums over the two lane halves of the query; lane l holds O^T dims 32 t + 8 (r / 4) + 4 hf + r % 4 of query
   // qi_lane
   l_run = pair32_sum(l_run);
-  if (qi_lane >= lq) return;
-  if (g.splits > 1) {  // this split's record of the query: the reference max, the row sum and O, unnormalised
-    if (q0s + qi_lane >= g.ws_rows) return;
-    float* rec = g.ws + ((int64_t(split) * g.ws_rows + q0s + qi_lane) * g.Hq + h) * record_len(D);
-    if (hf == 0) {
-      rec[0] = m_run;
-      rec[1] = l_run;
+  if (g.splits > 1) {
+    // this split's records of the wave's queries: the reference max and the row sum, and O unnormalised. O goes out
+    // in whole 128-byte lines written through the L2: each half of the dims passes through the wave's own part of
+    // the LDS (free after the loop's last barrier), a lane holding dims 32 t + 8 (r / 4) + 4 hf + r % 4 of its query
+    // and a store instruction then covering D / 2 consecutive floats of 64 * 16 / (2 D) queries. Stored from the
+    // MFMA layout (32-byte pieces of 32 records per instruction, (max, sum) beside O) the records' dirty lines were
+    // written back after the last block: a 256-token chunk over 3840 cached keys 34.1 -> 32.2 us, a fresh
+    // 2048-token prompt (2 splits) 62.7 -> 59.8 us, 256 over 1792 33.0 -> 29.8 us (whole lines with plain stores:
+    // 32.5 / 61.8 / 31.3 us).
+    const int nq = min(32, min(lq, int(min<int64_t>(g.ws_rows - q0s, INT32_MAX))) - wave_q0);  // wave-uniform
+    if (nq <= 0) return;
+    const int64_t rec0 = (int64_t(split) * g.ws_rows + q0s + wave_q0) * g.Hq + h;  // record of the first query
+    if (hf == 0 && ql < nq)
+      *reinterpret_cast<f32x2*>(g.ws + int64_t(g.splits) * g.ws_rows * g.Hq * D + 2 * (rec0 + int64_t(ql) * g.Hq)) =
+          f32x2{m_run, l_run};
+    constexpr int HD = D / 2, RP = HD + 4;  // dims per pass, LDS row pitch (floats)
+    constexpr int CH = HD / 4, PER = 32 * CH / 64;  // 16-byte chunks per query and pass, per lane and pass
+    static_assert(kThreads / 64 * 32 * RP * 4 <= LDS_ELEMS * 2, "record staging exceeds the LDS");
+    float* wl = reinterpret_cast<float*>(lds) + (tid / 64) * 32 * RP;
+#pragma unroll
+    for (int hv = 0; hv < 2; ++hv) {
+#pragma unroll
+      for (int t = hv * DT / 2; t < (hv + 1) * DT / 2; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          *reinterpret_cast<f32x4_t*>(wl + ql * RP + 32 * (t - hv * DT / 2) + 8 * rr + 4 * hf) =
+              f32x4_t{o[t][4 * rr], o[t][4 * rr + 1], o[t][4 * rr + 2], o[t][4 * rr + 3]};
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = lane + 64 * i, qq = c / CH, cc = c % CH;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(wl + qq * RP + 4 * cc);
+        if (qq < nq) store16_wt(g.ws + (rec0 + int64_t(qq) * g.Hq) * D + hv * HD + 4 * cc, x);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
     }
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        *reinterpret_cast<f32x4_t*>(rec + 4 + 32 * t + 8 * rr + 4 * hf) =
-            f32x4_t{o[t][4 * rr], o[t][4 * rr + 1], o[t][4 * rr + 2], o[t][4 * rr + 3]};
     return;
   }
+  if (qi_lane >= lq) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
   uint16_t* op = g.out + int64_t(q0s + qi_lane) * g.o_st + int64_t(h) * g.o_sh + 4 * hf;
 #pragma unroll
@@ -490,7 +518,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const Prefi
 // 3840 cached keys, 16 splits, read its 34.6 MB of records at ~5 TB/s.)
 template <int D>
 __global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int per_seq) {
-  constexpr int REC = record_len(D), DPL = D / 32, SB = 8;
+  constexpr int DPL = D / 32, SB = 8;
   static_assert(DPL == 2 || DPL == 4, "head_dim 64 or 128");
   const int b = blockIdx.x / per_seq;
   const int lane = threadIdx.x % 64, hh = lane / 32;
@@ -500,12 +528,13 @@ __global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int 
   const int64_t rows_left = min<int64_t>(lq, g.ws_rows - q0s);  // queries of the sequence that have records
   const bool ok0 = p0 < rows_left * g.Hq, ok1 = p0 + 1 < rows_left * g.Hq;
   if (!ok0) return;  // the wave's first pair is past the sequence's queries (wave-uniform)
-  const int64_t step = g.ws_rows * g.Hq * REC;  // one split further
-  const float* rec0 = g.ws + (int64_t(q0s) * g.Hq + p0) * REC;
+  const int64_t step = g.ws_rows * g.Hq;  // records of one split
+  const int64_t rec0 = int64_t(q0s) * g.Hq + p0;
+  const float* ml = g.ws + g.splits * step * D + 2 * rec0;  // (max, sum) of pair p0, split 0
   const bool mine = lane < g.splits;  // splits <= 64 (host)
   f32x2 ml0 = {-INFINITY, 0.0f}, ml1 = {-INFINITY, 0.0f};
-  if (mine) ml0 = *reinterpret_cast<const f32x2*>(rec0 + lane * step);
-  if (mine && ok1) ml1 = *reinterpret_cast<const f32x2*>(rec0 + REC + lane * step);
+  if (mine) ml0 = *reinterpret_cast<const f32x2*>(ml + 2 * lane * step);
+  if (mine && ok1) ml1 = *reinterpret_cast<const f32x2*>(ml + 2 + 2 * lane * step);
   float M0 = ml0[0], M1 = ml1[0];
 #pragma unroll
   for (int off = 32; off >= 1; off /= 2) M0 = fmaxf(M0, __shfl_xor(M0, off)), M1 = fmaxf(M1, __shfl_xor(M1, off));
@@ -515,7 +544,7 @@ __global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int 
 #pragma unroll
   for (int off = 32; off >= 1; off /= 2) den0 += __shfl_xor(den0, off), den1 += __shfl_xor(den1, off);
   const bool mine_pair = hh == 0 || ok1;
-  const float* rp = rec0 + hh * REC + 4 + (lane % 32) * DPL;
+  const float* rp = g.ws + (rec0 + hh) * D + (lane % 32) * DPL;
   float num[DPL] = {};
   for (int sp0 = 0; sp0 < g.splits; sp0 += SB) {
     float v[SB][DPL];
@@ -524,10 +553,10 @@ __global__ __launch_bounds__(256) void prefill_combine(const PrefillArgs g, int 
       const int sp = min(sp0 + u, g.splits - 1);
       if (mine_pair) {
         if constexpr (DPL == 4) {
-          const f32x4_t x = *reinterpret_cast<const f32x4_t*>(rp + sp * step);
+          const f32x4_t x = *reinterpret_cast<const f32x4_t*>(rp + sp * step * D);
           v[u][0] = x[0], v[u][1] = x[1], v[u][2] = x[2], v[u][3] = x[3];
         } else {
-          const f32x2 x = *reinterpret_cast<const f32x2*>(rp + sp * step);
+          const f32x2 x = *reinterpret_cast<const f32x2*>(rp + sp * step * D);
           v[u][0] = x[0], v[u][1] = x[1];
         }
       } else {

@@ -130,7 +130,7 @@ def test_attention_store_and_fused_gemm_reject_bad_arguments_without_launching()
 
     # key splits of the prefill attention: only when few blocks meet long key ranges
     pws = lib.nvhip_prefill_attention_workspace_size
-    rec = (128 + 4) * 4                                       # bytes of one (split, query, head) record
+    rec = (128 + 2) * 4                                       # bytes of one (split, query, head) record: O, max, sum
     dec = (2 + 128) * 4 * 16                                  # one short-sequence split record: 16 rows (8 queries x G 2)
     cnt = 2048                                                # the decode attention's counters, first
     # 4 x 16 query tiles x 8 head pairs fill the CUs: no prefill split, but room for the short-sequence path's
