@@ -642,6 +642,18 @@ def decode_attention(torch, dev, steps, g, batch=32, min_len=512, max_len=2048, 
             "context_tokens": ctx, "bytes": nbytes}
 
 
+def profile_warmup(torch, call):
+    """Eager calls until WARM_S of wall time has passed (the GPU raises its clocks over several milliseconds of
+    load), for the kernel traces: their summaries average the calls after these. Returns the number of calls."""
+    n, t0 = 0, time.perf_counter()
+    while n < 4 or time.perf_counter() - t0 < WARM_S:
+        for _ in range(4):
+            call()
+        n += 4
+        torch.cuda.synchronize()
+    return n
+
+
 def prefill_attention(torch, dev, steps, g, nseq=4, L=2048, profile=False):
     """Causal prefill attention of one Qwen3-0.6B layer over nseq sequences of L tokens (k, v views of the qkv
     output). flops = 4 * D * Hq * sum over queries of the keys each sees (L (L + 1) / 2 per sequence)."""
@@ -652,11 +664,12 @@ def prefill_attention(torch, dev, steps, g, nseq=4, L=2048, profile=False):
     k = buf[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D)
     v = buf[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].view(T, HKV, D)
     cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=dev)
-    if profile:  # for a rocprofv3 kernel trace: `steps` eager launches, nothing else launched
+    if profile:  # for a rocprofv3 kernel trace: warm-up launches (the clock ramp), then `steps` eager launches
+        warm = profile_warmup(torch, lambda: flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True))
         for _ in range(steps):
             flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True)
         torch.cuda.synchronize()
-        print(f"profile: {steps} prefill attention launches ({nseq} x {L} tokens)", flush=True)
+        print(f"profile: {warm} warm-up, then {steps} prefill attention launches ({nseq} x {L} tokens)", flush=True)
         return None
     ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, k, v, L, cu, L, cu, D ** -0.5, True), 4,
                        max(20, steps // 4), 4, WARM_S)
@@ -678,11 +691,13 @@ def prefill_chunk_over_prefix(torch, dev, steps, g, chunk=256, prefix=3840, prof
     q = torch.randn(chunk, HQ, D, generator=g).to(torch.bfloat16).to(dev)
     cq = torch.tensor([0, chunk], dtype=torch.int32, device=dev)
     ck = torch.tensor([0, lk], dtype=torch.int32, device=dev)
-    if profile:  # for a rocprofv3 kernel trace: `steps` eager calls, nothing else launched
+    if profile:  # for a rocprofv3 kernel trace: warm-up calls (the clock ramp), then `steps` eager calls
+        warm = profile_warmup(torch, lambda: flash_attn_varlen_func(q, kc, vc, chunk, cq, lk, ck, D ** -0.5, True, bt))
         for _ in range(steps):
             flash_attn_varlen_func(q, kc, vc, chunk, cq, lk, ck, D ** -0.5, True, bt)
         torch.cuda.synchronize()
-        print(f"profile: {steps} prefill attention calls ({chunk}-token chunk over {prefix} cached keys)", flush=True)
+        print(f"profile: {warm} warm-up, then {steps} prefill attention calls ({chunk}-token chunk over {prefix} "
+              f"cached keys)", flush=True)
         return None
     ms, _ = time_graph(torch, lambda i: flash_attn_varlen_func(q, kc, vc, chunk, cq, lk, ck, D ** -0.5, True, bt), 4,
                        max(20, steps // 4), 4, WARM_S)
