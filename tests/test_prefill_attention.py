@@ -177,6 +177,39 @@ def test_out_buffer_gets_the_same_rows():
     assert torch.all(buf[:2] == 7) and torch.all(buf[2 + q.shape[0]:] == 7)
 
 
+@pytest.mark.parametrize("layout", ["head_stride_132", "offset_8_bytes"])
+def test_out_not_in_16_byte_pieces(layout):
+    """An out buffer whose rows do not start on 16-byte boundaries (head stride 132, or the whole view 8 bytes off)
+    takes the kernel's per-lane 8-byte stores instead of the rows staged through the LDS and stored as whole lines:
+    the same bits either way, for contiguous keys (causal, partial query tiles) and for keys split over blocks."""
+    for split in (False, True):
+        if split:
+            lq, lk = [256], [4096]
+            q, kc, vc, bt = paged_case(lq, lk, 256, seed=21)
+            args = (max(lq), cu(lq).to(DEV), max(lk), cu(lk).to(DEV), 128 ** -0.5, True, bt.to(DEV))
+            q, k, v = q.to(DEV), kc.to(DEV), vc.to(DEV)
+        else:
+            lens = [70, 300, 129]
+            _, q, k, v = contiguous_case(lens, seed=22)
+            q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+            args = (max(lens), cu(lens).to(DEV), max(lens), cu(lens).to(DEV), 128 ** -0.5, True)
+        want = flash_attn_varlen_func(q, k, v, *args)
+        T = q.shape[0]
+        if layout == "head_stride_132":
+            buf = torch.full((T, 16, 132), 7.0, dtype=torch.bfloat16, device=DEV)
+            out = buf[:, :, :128]
+        else:
+            buf = torch.full((T * 16 * 128 + 4,), 7.0, dtype=torch.bfloat16, device=DEV)
+            out = buf[4:].view(T, 16, 128)
+            assert out.data_ptr() % 16 == 8
+        got = flash_attn_varlen_func(q, k, v, *args, out=out)
+        assert got.data_ptr() == out.data_ptr() and torch.equal(got, want)
+        if layout == "head_stride_132":
+            assert torch.all(buf[:, :, 128:] == 7)
+        else:
+            assert torch.all(buf[:4] == 7)
+
+
 def test_chunk_over_a_long_prefix_splits_the_keys():
     """A 256-token chunk over 3840 cached keys: 16 blocks would stream 4096 keys each, so the call splits the keys
     into 16 ranges (256 blocks) and merges them (workspace query pinned on the CPU)."""
