@@ -1223,13 +1223,21 @@ int launch_mfma(const MfmaArgs& g, hipStream_t s) {
 // When 64x64 tiles fit in one round (M <= 64, or mixed steps and prefill chunks of up to a few hundred rows) a
 // block's time is its chain of K / 64 k-tiles, each waiting on its loads: 64x64 tiles with 4 k-tiles of loads in
 // flight (RS = 4) instead of 2 (M = 256: down 22.6 -> 15.8 us, o_proj 15.4 -> 11.0, qkv 9.9 -> 7.4; deeper
-// staging measured no faster, and none of it helps once every CU has a large tile). The k order of every tile
+// staging measured no faster, and none of it helps once every CU has a large tile), and 32x64 tiles where those
+// still fit one round (more blocks, each streaming fewer bytes). The k order of every tile
 // shape is the same, so the result does not depend on the choice.
 template <int RS, bool KTAIL, bool SILU, bool BNM = false>
 int launch_mfma_shape(const MfmaArgs& g, hipStream_t s) {
   constexpr int kCUs = 256;
   const int64_t tiles64 = int64_t((g.M + 63) / 64) * ((g.N + 63) / 64);
   if (g.M <= 64 || tiles64 <= kCUs) {
+    // 32 x 64 tiles (2 waves) when they still fit one round: twice the blocks of 64 x 64 (K = 1024, weights from
+    // HBM: qkv M = 48 / 64 / 96 / 128 7.2 / 7.7 / 7.2 / 7.5 -> 6.4 / 6.6 / 6.5 / 6.5 us, gate_up M = 48 / 64 7.5 /
+    // 7.9 -> 6.5 / 6.8 us); past one round (or with 8 k-tiles in flight) they measured slower
+    const int64_t tiles32 = int64_t((g.M + 31) / 32) * ((g.N + 63) / 64);
+    if constexpr (!KTAIL)
+      if (g.M > 32 && tiles32 <= kCUs && ((g.K / kBK) & 3) == 0)
+        return launch_mfma<32, 64, 1, 2, 4, false, SILU, BNM>(g, s);
     if constexpr (!KTAIL)
       if (((g.K / kBK) & 3) == 0) return launch_mfma<64, 64, 2, 2, 4, false, SILU, BNM>(g, s);
     return launch_mfma<64, 64, 2, 2, RS, KTAIL, SILU, BNM>(g, s);
