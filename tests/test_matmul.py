@@ -29,7 +29,7 @@ TOL = {
 }
 DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16}
 SHAPES = [(1, 1024, 4096), (1, 3072, 1024), (7, 33, 65), (17, 129, 257), (100, 300, 70), (127, 255, 1000),
-          (512, 512, 512), (1000, 1000, 1000), (3, 5, 2), (130, 260, 36), (20, 100, 200)]
+          (512, 512, 512), (1000, 1000, 1000), (3, 5, 2), (130, 260, 36), (20, 100, 200), (77, 1000, 1024)]
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "matmul_small.npz")
 
 
@@ -101,9 +101,10 @@ def test_qwen_projection_shapes(layer, M):
 
 @pytest.mark.parametrize("layer", list(QWEN_SHAPES))
 def test_rows_do_not_depend_on_the_tile_choice(layer):
-    """Every MFMA tile shape (64x64 with 4 k-tiles of loads in flight while 64x64 tiles fit one round on the CUs,
+    """Every MFMA tile shape (32x64 or 64x64 with 4 k-tiles of loads in flight while they fit one round on the CUs,
     the cost model's larger tiles beyond) sums each output in the same k order, so a row of C has the same bits
-    whatever M selects: rows of products with 100, 256 and 512 rows equal those rows of the 2048-row product. With
+    whatever M selects: rows of products with 48, 64, 100, 256 and 512 rows equal those rows of the 2048-row
+    product. With
     K >= 2048 (down, o_proj) up to 256 rows run the skinny kernels' row tiles instead, whose block shapes also share
     one k order: there rows of 100- and 256-row products equal those of the 64-row product, and 512 rows equal the
     2048-row product."""
@@ -121,7 +122,7 @@ def test_rows_do_not_depend_on_the_tile_choice(layer):
             ref = oracle.matmul_fp64(a[:M].cpu(), w.cpu().t())
             torch.testing.assert_close(c.cpu().double(), ref, rtol=1.6e-2, atol=1e-2)
         return
-    for M in (100, 256, 512):
+    for M in (48, 64, 100, 256, 512):
         assert torch.equal(matmul(a[:M], w.t()), full[:M]), M
 
 
