@@ -329,12 +329,11 @@ def time_steps(torch, fn, steps, warmup, min_warm_s, lead=64):
     replays and than eager calls, whose time matches the kernel trace's mean duration."""
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    i, t0 = 0, time.perf_counter()
-    while i < warmup or time.perf_counter() - t0 < min_warm_s:
-        fn(i)
-        i += 1
-        if i % 256 == 0:
-            torch.cuda.synchronize()
+    # the lead-in graph is recorded first, so that nothing leaves the GPU idle between the warm-up calls, the lead-in
+    # replay and the timed calls (recording it after the warm-up left the GPU idle for the few milliseconds the
+    # recording takes, and the timed calls then started on a cooling clock)
+    fn(0)  # one eager call before the recording (lazy set-up happens outside it)
+    torch.cuda.synchronize()
     s = torch.cuda.Stream()
     s.wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
@@ -343,6 +342,12 @@ def time_steps(torch, fn, steps, warmup, min_warm_s, lead=64):
             for j in range(lead):
                 fn(j)
     torch.cuda.synchronize()
+    i, t0 = 0, time.perf_counter()
+    while i < warmup or time.perf_counter() - t0 < min_warm_s:
+        fn(i)
+        i += 1
+        if i % 256 == 0:
+            torch.cuda.synchronize()
     graph.replay()
     start.record(stream)
     h0 = time.perf_counter()
