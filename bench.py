@@ -573,10 +573,10 @@ def extras(torch, oracle, kernels, dev, steps):
     del a, b
     # decode-sized GEMMs are weight-bandwidth bound: rotate over enough weight copies (>= 512 MiB) that every call
     # reads its weight from HBM, as a decode step over 28 layers does
-    # M = 32 (a decode batch), and M = 64 for the long-K projections (a batch of 33-64 rows; their inputs from a
-    # generator of their own, so the extras after them see the same inputs as without them)
+    # M = 32 (a decode batch), and M = 64 (a batch of 33-64 rows; their inputs from a generator of their own, so the
+    # extras after them see the same inputs as without them)
     g64 = torch.Generator().manual_seed(64)
-    for layer, M in [(name, 32) for name in GEMM_SHAPES] + [("down", 64), ("o_proj", 64)]:
+    for layer, M in [(name, 32) for name in GEMM_SHAPES] + [(name, 64) for name in GEMM_SHAPES]:
         K, N = GEMM_SHAPES[layer]
         nw = -(-(512 * 2 ** 20) // (N * K * 2))
         gl = g if M == 32 else g64
